@@ -1,0 +1,91 @@
+// Activation preparation kernels: Q8_1 quantization and the h16 (block-scaled FP16) pre-pass.
+//
+// Each 32-element activation block is handled by one half of a wave64 (32 lanes, one element per lane);
+// the block reductions are the xor butterfly over those 32 lanes with offsets 16, 8, 4, 2, 1, the exact
+// FP32 order of the reference (src/reference/qmv_model.cpp:44-52). Since a+b == b+a in IEEE arithmetic,
+// every lane of the half ends with the same, order-defined sum.
+#include "common.h"
+#include "launch.h"
+
+namespace p1x {
+namespace {
+
+__device__ __forceinline__ float half_max(float v) {
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ float half_sum(float v) {
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ int half_isum(int v) {
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// Q8_1 (qmv_model.cpp:60-68, quantize.cu:88-110): d = amax/127 (IEEE division), q = round(x/d) with ties
+// away from zero, s = fp16(sum of the original x), plus the exact integer sum of q for k-quant minima.
+// Grid (ceil(K/256), ncols); K % 32 == 0, so the lanes past K are whole 32-lane halves that exit together.
+__global__ __launch_bounds__(256) void k_quantize_q8_1(const float* __restrict__ x, int8_t* __restrict__ qs,
+                                                       float4* __restrict__ ds, int K) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= K) return;
+    const size_t col = blockIdx.y;
+    const float v = x[col * K + i];
+    const float amax = half_max(fabsf(v));
+    const float d = amax / 127.0f;
+    const int q = amax == 0.0f ? 0 : static_cast<int>(roundf(v / d));
+    qs[col * K + i] = static_cast<int8_t>(q);
+    const float s = half_sum(v);
+    const int isum = half_isum(q);
+    if ((threadIdx.x & 31) == 0)
+        ds[col * (K / 32) + i / 32] = make_float4(round_fp16(d), round_fp16(s), static_cast<float>(isum), 0.0f);
+}
+
+// h16 pre-pass (qmv_model.cpp:57-68; 0005 patch :185-207): s = amax, x^ = fp16(x/s) stored at the permuted
+// position (index bits 0 and 1 swapped), sum = butterfly sum of the fp16 values in FP32.
+__global__ __launch_bounds__(256) void k_prepare_h16(const float* __restrict__ x, uint16_t* __restrict__ h,
+                                                     float2* __restrict__ meta, int K) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= K) return;
+    const size_t col = blockIdx.y;
+    const float v = x[col * K + i];
+    const float s = half_max(fabsf(v));
+    const __half hv = __float2half(s == 0.0f ? 0.0f : v / s);
+    const int lane = i & 31;
+    const int p = (lane & ~3) | ((lane & 1) << 1) | ((lane & 2) >> 1);
+    h[col * K + (i - lane) + p] = __half_as_ushort(hv);
+    const float sum = half_sum(__half2float(hv));
+    if (lane == 0) meta[col * (K / 32) + i / 32] = make_float2(s, sum);
+}
+
+__global__ __launch_bounds__(256) void k_round_fp16(const float* __restrict__ x, uint16_t* __restrict__ out,
+                                                    int64_t n) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i < n) out[i] = __half_as_ushort(__float2half(x[i]));
+}
+
+}  // namespace
+
+hipError_t launch_quantize_q8_1(const float* x, int8_t* qs, float* ds, int K, int ncols, hipStream_t stream) {
+    const dim3 grid((K + 255) / 256, ncols);
+    hipLaunchKernelGGL(k_quantize_q8_1, grid, dim3(256), 0, stream, x, qs, reinterpret_cast<float4*>(ds), K);
+    return hipGetLastError();
+}
+
+hipError_t launch_prepare_h16(const float* x, uint16_t* h, float* meta, int K, int ncols, hipStream_t stream) {
+    const dim3 grid((K + 255) / 256, ncols);
+    hipLaunchKernelGGL(k_prepare_h16, grid, dim3(256), 0, stream, x, h, reinterpret_cast<float2*>(meta), K);
+    return hipGetLastError();
+}
+
+hipError_t launch_round_fp16(const float* x, uint16_t* out, int64_t n, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+    hipLaunchKernelGGL(k_round_fp16, grid, dim3(256), 0, stream, x, out, n);
+    return hipGetLastError();
+}
+
+}  // namespace p1x

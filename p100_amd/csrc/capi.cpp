@@ -1,0 +1,256 @@
+// C ABI of the decode hot path (include/p1x.h): argument checks, workspace sizing and kernel dispatch.
+// Errors mirror the reference's conventions: attention parameter checks return the exact reason strings of
+// p100::validate (src/reference/attention_reference.cpp:18-32); GPU errors carry the HIP error text.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "../../include/p1x.h"
+
+#include "launch.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const std::string& why) {
+    g_error = why;
+    return code;
+}
+int hip_fail(hipError_t e, const char* what) {
+    return fail(P1X_EHIP, std::string(what) + ": " + hipGetErrorName(e) + ": " + hipGetErrorString(e));
+}
+
+std::once_flag g_once;
+int g_init_status = P1X_OK;
+std::string g_init_error;
+
+void init_once() {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        g_init_status = P1X_EHIP;
+        g_init_error = std::string("hipGetDevice: ") + hipGetErrorString(e);
+        return;
+    }
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, dev);
+    if (e != hipSuccess) {
+        g_init_status = P1X_EHIP;
+        g_init_error = std::string("hipGetDeviceProperties: ") + hipGetErrorString(e);
+        return;
+    }
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        g_init_status = P1X_EUNSUPPORTED;
+        g_init_error = std::string("this library is built for gfx950 only; device 0 is ") + prop.gcnArchName;
+    }
+}
+
+int ensure_init() {
+    std::call_once(g_once, init_once);
+    if (g_init_status != P1X_OK) return fail(g_init_status, g_init_error);
+    return P1X_OK;
+}
+
+int block_elems(int t) { return (t == P1X_Q4_K || t == P1X_Q6_K) ? 256 : 32; }
+int block_bytes(int t) {
+    switch (t) {
+        case P1X_Q4_0: return 18;
+        case P1X_Q8_0: return 34;
+        case P1X_Q4_K: return 144;
+        case P1X_Q6_K: return 210;
+    }
+    return 0;
+}
+
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+size_t q8_1_bytes(int64_t K, int64_t ncols) { return align256(size_t(K) * ncols) + align256(size_t(K / 32) * ncols * 16); }
+size_t h16_bytes(int64_t K, int64_t ncols) { return align256(size_t(K) * ncols * 2) + align256(size_t(K / 32) * ncols * 8); }
+
+bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0; }
+
+int check_matvec(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K, int64_t ncols, const float* y) {
+    if (block_bytes(wtype) == 0) return fail(P1X_EUNSUPPORTED, "unsupported weight type " + std::to_string(wtype));
+    if (!w || !y) return fail(P1X_EINVAL, "null weight or output pointer");
+    if (M <= 0 || K <= 0 || M > INT32_MAX || K > INT32_MAX) return fail(P1X_EINVAL, "M and K must be in 1..INT_MAX");
+    if (K % block_elems(wtype)) return fail(P1X_EINVAL, "K must be a multiple of the block size");
+    if (ncols < 1 || ncols > 8) return fail(P1X_EINVAL, "ncols (ne11) must be 1..8");
+    if (nb01 < K / block_elems(wtype) * block_bytes(wtype)) return fail(P1X_EINVAL, "row stride nb01 shorter than a row");
+    if (nb01 % 2) return fail(P1X_EINVAL, "row stride nb01 must be even (GGUF blocks are 2-byte aligned)");
+    if ((wtype == P1X_Q4_K) && nb01 % 4) return fail(P1X_EINVAL, "q4_K row stride must be a multiple of 4");
+    if (!aligned(w, 4)) return fail(P1X_EINVAL, "weights must be 4-byte aligned");
+    return P1X_OK;
+}
+
+const char* attn_reason(const p1x_attn_params* p) {
+    if (p->batch <= 0 || p->n_head_q <= 0 || p->n_head_kv <= 0 || p->seq_q <= 0 || p->seq_kv <= 0 || p->d_qk <= 0 ||
+        p->d_v <= 0)
+        return "all dimensions must be positive";
+    if (p->n_head_q % p->n_head_kv != 0) return "n_head_q must be divisible by n_head_kv";
+    if (p->softcap < 0.0f || !std::isfinite(p->softcap)) return "softcap must be finite and non-negative";
+    if (!std::isfinite(p->scale)) return "scale must be finite";
+    return nullptr;
+}
+
+}  // namespace
+
+extern "C" {
+
+int p1x_version(void) { return 100; }
+
+int p1x_init(void) { return ensure_init(); }
+
+const char* p1x_last_error(void) { return g_error.c_str(); }
+
+int p1x_quantize_q8_1(const float* x, int8_t* qs, float* ds, int64_t K, int64_t ncols, void* stream) {
+    if (int rc = ensure_init()) return rc;
+    if (!x || !qs || !ds) return fail(P1X_EINVAL, "null pointer");
+    if (K <= 0 || K % 32 || K > INT32_MAX) return fail(P1X_EINVAL, "K must be a positive multiple of 32");
+    if (ncols < 1 || ncols > 65535) return fail(P1X_EINVAL, "ncols must be 1..65535");
+    if (!aligned(qs, 16) || !aligned(ds, 16)) return fail(P1X_EINVAL, "qs and ds must be 16-byte aligned");
+    hipError_t e = p1x::launch_quantize_q8_1(x, qs, ds, int(K), int(ncols), static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? P1X_OK : hip_fail(e, "quantize_q8_1");
+}
+
+int p1x_prepare_h16(const float* x, uint16_t* h, float* meta, int64_t K, int64_t ncols, void* stream) {
+    if (int rc = ensure_init()) return rc;
+    if (!x || !h || !meta) return fail(P1X_EINVAL, "null pointer");
+    if (K <= 0 || K % 32 || K > INT32_MAX) return fail(P1X_EINVAL, "K must be a positive multiple of 32");
+    if (ncols < 1 || ncols > 65535) return fail(P1X_EINVAL, "ncols must be 1..65535");
+    if (!aligned(h, 16) || !aligned(meta, 8)) return fail(P1X_EINVAL, "h must be 16-byte and meta 8-byte aligned");
+    hipError_t e = p1x::launch_prepare_h16(x, h, meta, int(K), int(ncols), static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? P1X_OK : hip_fail(e, "prepare_h16");
+}
+
+size_t p1x_mul_mat_vec_workspace(int wtype, int64_t M, int64_t K, int64_t ncols, int act_mode) {
+    (void)wtype;
+    (void)M;
+    if (K <= 0 || ncols <= 0) return 0;
+    return act_mode == P1X_ACT_H16 ? h16_bytes(K, ncols) : q8_1_bytes(K, ncols);
+}
+
+int p1x_mul_mat_vec_q8_1(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K, const int8_t* qs,
+                         const float* ds, int64_t ncols, float* y, int32_t* group_sums, void* stream) {
+    if (int rc = ensure_init()) return rc;
+    if (int rc = check_matvec(wtype, w, nb01, M, K, ncols, y)) return rc;
+    if (!qs || !ds) return fail(P1X_EINVAL, "null activation pointer");
+    if (!aligned(qs, 16) || !aligned(ds, 16)) return fail(P1X_EINVAL, "qs and ds must be 16-byte aligned");
+    hipError_t e = p1x::launch_mmvq(wtype, int(ncols), w, nb01, int(M), int(K), qs, ds, y, group_sums,
+                                    static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? P1X_OK : hip_fail(e, "mul_mat_vec_q8_1");
+}
+
+int p1x_mul_mat_vec_h16(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K, const uint16_t* h,
+                        const float* meta, int64_t ncols, float* y, void* stream) {
+    if (int rc = ensure_init()) return rc;
+    if (int rc = check_matvec(wtype, w, nb01, M, K, ncols, y)) return rc;
+    if (!h || !meta) return fail(P1X_EINVAL, "null activation pointer");
+    if (!aligned(h, 16) || !aligned(meta, 8)) return fail(P1X_EINVAL, "h must be 16-byte and meta 8-byte aligned");
+    hipError_t e = p1x::launch_mmvh(wtype, int(ncols), w, nb01, int(M), int(K), h, meta, y,
+                                    static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? P1X_OK : hip_fail(e, "mul_mat_vec_h16");
+}
+
+int p1x_mul_mat_vec(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K, int act_mode, const float* x,
+                    int64_t ncols, float* y, int32_t* group_sums, void* ws, size_t ws_bytes, void* stream) {
+    if (int rc = ensure_init()) return rc;
+    if (int rc = check_matvec(wtype, w, nb01, M, K, ncols, y)) return rc;
+    if (!x) return fail(P1X_EINVAL, "null activation pointer");
+    if (act_mode != P1X_ACT_Q8_1 && act_mode != P1X_ACT_H16) return fail(P1X_EINVAL, "unknown activation mode");
+    if (act_mode == P1X_ACT_H16 && group_sums)
+        return fail(P1X_EINVAL, "group sums exist only for the Q8_1 activation mode");
+    const size_t need = p1x_mul_mat_vec_workspace(wtype, M, K, ncols, act_mode);
+    if (!ws || ws_bytes < need)
+        return fail(P1X_EWORKSPACE, "workspace of " + std::to_string(need) + " bytes required");
+    if (!aligned(ws, 256)) return fail(P1X_EINVAL, "workspace must be 256-byte aligned");
+    auto* base = static_cast<uint8_t*>(ws);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (act_mode == P1X_ACT_Q8_1) {
+        auto* qs = reinterpret_cast<int8_t*>(base);
+        auto* ds = reinterpret_cast<float*>(base + align256(size_t(K) * ncols));
+        hipError_t e = p1x::launch_quantize_q8_1(x, qs, ds, int(K), int(ncols), s);
+        if (e != hipSuccess) return hip_fail(e, "quantize_q8_1");
+        e = p1x::launch_mmvq(wtype, int(ncols), w, nb01, int(M), int(K), qs, ds, y, group_sums, s);
+        return e == hipSuccess ? P1X_OK : hip_fail(e, "mul_mat_vec_q8_1");
+    }
+    auto* h = reinterpret_cast<uint16_t*>(base);
+    auto* meta = reinterpret_cast<float*>(base + align256(size_t(K) * ncols * 2));
+    hipError_t e = p1x::launch_prepare_h16(x, h, meta, int(K), int(ncols), s);
+    if (e != hipSuccess) return hip_fail(e, "prepare_h16");
+    e = p1x::launch_mmvh(wtype, int(ncols), w, nb01, int(M), int(K), h, meta, y, s);
+    return e == hipSuccess ? P1X_OK : hip_fail(e, "mul_mat_vec_h16");
+}
+
+int p1x_attn_validate(const p1x_attn_params* p) {
+    if (!p) return fail(P1X_EINVAL, "null parameters");
+    if (const char* why = attn_reason(p)) return fail(P1X_EINVAL, why);
+    g_error.clear();
+    return P1X_OK;
+}
+
+size_t p1x_flash_attn_decode_workspace(const p1x_attn_params* p) {
+    if (!p || attn_reason(p)) return 0;
+    int splits = 0, chunk = 0;
+    p1x::fa_split_plan(p->batch, p->n_head_q, p->n_head_kv, p->seq_q, p->seq_kv, splits, chunk);
+    return size_t(p->batch) * p->n_head_q * p->seq_q * splits * (p->d_v + 2) * sizeof(float);
+}
+
+int p1x_flash_attn_decode(const p1x_attn_params* p, const float* q, const uint16_t* k, const uint16_t* v,
+                          const p1x_kv_strides* strides, const float* mask, float* o, float* lse, void* ws,
+                          size_t ws_bytes, void* stream) {
+    if (int rc = ensure_init()) return rc;
+    if (int rc = p1x_attn_validate(p)) return rc;
+    if (!q || !k || !v || !o) return fail(P1X_EINVAL, "null q, k, v or o pointer");
+    if (p->d_qk != p->d_v || (p->d_qk != 64 && p->d_qk != 128 && p->d_qk != 256))
+        return fail(P1X_EUNSUPPORTED, "decode kernel supports d_qk == d_v in {64, 128, 256}");
+    if (p->seq_q > 65535 || int64_t(p->batch) * p->n_head_kv > 65535)
+        return fail(P1X_EUNSUPPORTED, "seq_q and batch*n_head_kv must be <= 65535");
+    if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16))
+        return fail(P1X_EINVAL, "q, k and v must be 16-byte aligned");
+    const int64_t d = p->d_qk;
+    p1x::FaArgs a{};
+    a.q = q;
+    a.k = reinterpret_cast<const __half*>(k);
+    a.v = reinterpret_cast<const __half*>(v);
+    a.mask = mask;
+    a.part = static_cast<float*>(ws);
+    if (strides) {
+        a.k_row = strides->k_row, a.k_head = strides->k_head, a.k_batch = strides->k_batch;
+        a.v_row = strides->v_row, a.v_head = strides->v_head, a.v_batch = strides->v_batch;
+        if (a.k_row % 8 || a.k_head % 8 || a.k_batch % 8 || a.v_row % 8 || a.v_head % 8 || a.v_batch % 8)
+            return fail(P1X_EINVAL, "K/V element strides must be multiples of 8 (16-byte rows)");
+        if (a.k_row < d || a.v_row < d) return fail(P1X_EINVAL, "K/V row stride shorter than a row");
+    } else {
+        a.k_row = a.v_row = d;
+        a.k_head = a.v_head = d * p->seq_kv;
+        a.k_batch = a.v_batch = d * p->seq_kv * p->n_head_kv;
+    }
+    a.hq = p->n_head_q;
+    a.hkv = p->n_head_kv;
+    a.seq_q = p->seq_q;
+    a.seq_kv = p->seq_kv;
+    a.causal = p->causal != 0;
+    a.scale = p->scale == 0.0f ? 1.0f / std::sqrt(float(p->d_qk)) : p->scale;
+    a.softcap = p->softcap;
+    p1x::fa_split_plan(p->batch, p->n_head_q, p->n_head_kv, p->seq_q, p->seq_kv, a.splits, a.chunk);
+    const size_t need = p1x_flash_attn_decode_workspace(p);
+    if (!ws || ws_bytes < need)
+        return fail(P1X_EWORKSPACE, "workspace of " + std::to_string(need) + " bytes required");
+    if (!aligned(ws, 16)) return fail(P1X_EINVAL, "workspace must be 16-byte aligned");
+    hipError_t e = p1x::launch_fa_decode(a, p->batch, p->d_qk, o, lse, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? P1X_OK : hip_fail(e, "flash_attn_decode");
+}
+
+int p1x_round_to_fp16(const float* x, uint16_t* out, int64_t n, void* stream) {
+    if (int rc = ensure_init()) return rc;
+    if (!x || !out || n < 0) return fail(P1X_EINVAL, "invalid arguments");
+    if (n == 0) return P1X_OK;
+    hipError_t e = p1x::launch_round_fp16(x, out, n, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? P1X_OK : hip_fail(e, "round_to_fp16");
+}
+
+}  // extern "C"

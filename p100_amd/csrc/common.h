@@ -1,0 +1,104 @@
+// Device helpers shared by the gfx950 kernels (wave64, CDNA4).
+#pragma once
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace p1x {
+
+constexpr int kWave = 64;
+
+// GGUF block geometry (ggml-common.h): elements and bytes per block.
+enum WType { Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q6_K = 14 };
+
+// Four dwords read with one global_load_dwordx4 at any 4-byte alignment (GGUF blocks are 2-byte aligned;
+// callers round the address down to a dword and re-slice with v_perm_b32).
+struct __attribute__((aligned(4))) U32x4 {
+    uint32_t x, y, z, w;
+};
+__device__ __forceinline__ U32x4 ld_u32x4(const uint32_t* p) { return *reinterpret_cast<const U32x4*>(p); }
+
+// Packed signed int8 dot product with int32 accumulate: v_dot4_i32_i8 (exact).
+__device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// Bytes sel[i] of the 8-byte value {hi:lo} (v_perm_b32).
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// Selector that extracts 4 consecutive bytes starting at byte offset `shift` (0 or 2) of {hi:lo}.
+__device__ __forceinline__ uint32_t slice_sel(uint32_t shift) { return shift ? 0x07060504u : 0x05040302u; }
+
+// GGUF q4_0 / q8_0 blocks sit at 2-byte alignment (18 / 34-byte strides). Both loaders read whole dwords
+// starting at the dword that holds the block's first byte, so every dword read holds at least one byte of the
+// block: a read never leaves the block's pages. q receives the quant bytes re-sliced to dwords, d the fp16 bits.
+__device__ __forceinline__ void load_q4_0_block(const uint8_t* p, uint32_t q[4], uint32_t& d) {
+    const uintptr_t addr = reinterpret_cast<uintptr_t>(p);
+    const uint32_t* base = reinterpret_cast<const uint32_t*>(addr & ~uintptr_t(3));
+    const uint32_t sh = uint32_t(addr & 2);
+    const U32x4 v = ld_u32x4(base);
+    const uint32_t w4 = base[4];
+    const uint32_t sel = slice_sel(sh);
+    q[0] = perm(v.y, v.x, sel);
+    q[1] = perm(v.z, v.y, sel);
+    q[2] = perm(v.w, v.z, sel);
+    q[3] = perm(w4, v.w, sel);
+    d = sh ? (v.x >> 16) : (v.x & 0xffffu);
+}
+__device__ __forceinline__ void load_q8_0_block(const uint8_t* p, uint32_t q[8], uint32_t& d) {
+    const uintptr_t addr = reinterpret_cast<uintptr_t>(p);
+    const uint32_t* base = reinterpret_cast<const uint32_t*>(addr & ~uintptr_t(3));
+    const uint32_t sh = uint32_t(addr & 2);
+    const U32x4 v0 = ld_u32x4(base), v1 = ld_u32x4(base + 4);
+    const uint32_t w[9] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w, base[8]};
+    const uint32_t sel = slice_sel(sh);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q[j] = perm(w[j + 1], w[j], sel);
+    d = sh ? (v0.x >> 16) : (v0.x & 0xffffu);
+}
+
+// A 2-byte aligned field of 4*N bytes strictly inside a block (N+1 dwords read from the dword holding its
+// first byte, the last of which still holds the field's last byte or the block's next bytes), re-sliced.
+template <int N>
+__device__ __forceinline__ void load_field(const uint8_t* p, uint32_t* out) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t* base = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+    uint32_t w[N + 1];
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+        const U32x4 v = ld_u32x4(base + i);
+        w[i] = v.x;
+        w[i + 1] = v.y;
+        w[i + 2] = v.z;
+        w[i + 3] = v.w;
+    }
+    w[N] = base[N];
+    const uint32_t sel = slice_sel(uint32_t(a & 2));
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = perm(w[i + 1], w[i], sel);
+}
+
+// The 16 bits at a 2-byte aligned address (a scale inside a block).
+__device__ __forceinline__ uint32_t load_u16(const uint8_t* p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    return (*reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3)) >> (8 * (a & 2))) & 0xffffu;
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
+    return __half2float(__ushort_as_half(static_cast<unsigned short>(bits16 & 0xffffu)));
+}
+__device__ __forceinline__ float round_fp16(float x) { return __half2float(__float2half(x)); }
+
+// Sum over the 64 lanes of a wave; every lane gets the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+// Sum over aligned groups of `width` lanes (power of two <= 64); every lane gets its group's total.
+__device__ __forceinline__ float group_sum(float v, int width) {
+    for (int o = width >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+}  // namespace p1x

@@ -1,0 +1,31 @@
+// Host-side launchers of the gfx950 kernels, called by the C ABI layer (capi.cpp).
+#pragma once
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace p1x {
+
+hipError_t launch_quantize_q8_1(const float* x, int8_t* qs, float* ds, int K, int ncols, hipStream_t stream);
+hipError_t launch_prepare_h16(const float* x, uint16_t* h, float* meta, int K, int ncols, hipStream_t stream);
+hipError_t launch_round_fp16(const float* x, uint16_t* out, int64_t n, hipStream_t stream);
+hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
+                       float* y, int32_t* gs, hipStream_t stream);
+hipError_t launch_mmvh(int type, int B, const void* w, int64_t nb01, int M, int K, const uint16_t* h,
+                       const float* meta, float* y, hipStream_t stream);
+
+// Pass-1 arguments of the split-K decode attention (fattn.hip).
+struct FaArgs {
+    const float* q;
+    const __half* k;
+    const __half* v;
+    const float* mask;
+    float* part;  // [rows][splits][D + 2]: unnormalised O, base-2 max, sum
+    int64_t k_row, k_head, k_batch, v_row, v_head, v_batch;  // element strides
+    int hq, hkv, seq_q, seq_kv, causal, splits, chunk, head_chunks;
+    float scale, softcap;
+};
+hipError_t launch_fa_decode(FaArgs a, int batch, int d, float* o, float* lse, hipStream_t stream);
+void fa_split_plan(int batch, int hq, int hkv, int seq_q, int seq_kv, int& splits, int& chunk);
+
+}  // namespace p1x

@@ -1,0 +1,222 @@
+"""GPU parity of the mat-vec path against the CPU oracle on identical seeded inputs.
+
+Bars (the north star's, written here):
+* Q8_1 activation (q, d, s and the integer sum) and the h16 pre-pass: bit-exact with the oracle's prepare().
+* int32 group sums of the Q8_1 path: bit-exact.
+* FP32 outputs: |y - oracle| <= 1e-5 * ||w_row|| * ||x|| against the oracle's value of the same path (same
+  formulas, different FP32 summation order), and |y - exact| <= 1e-3 * ||w_row|| * ||x|| against FP64
+  (tests/h2_mmv_gpu.cu:89,138-142 use the second form).
+Shapes follow tests/h2_mmv_gpu.cu:90-103: K in {1 block, 2 blocks, 4096, 14336}, 17 rows (a non-multiple tail),
+ncols 1..8, an all-zero activation block and a x50 outlier; plus the activation ranges x1e5 / x1e-5 of the
+reference's bench-only 0003 patch and rows whose 2-byte block alignment alternates.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TYPES = ["q4_0", "q8_0", "q4_K", "q6_K"]
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+def to_dev(a):
+    torch = _torch()
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def make_case(orc, t, k, rows, ncols, seed, scale=1.0):
+    rng = orc.Rng(seed)
+    w = np.stack([rng.random_row(t, k) for _ in range(rows)])
+    x = rng.normal(ncols * k).reshape(ncols, k).astype(np.float32)
+    x[:, :32] = 0  # one all-zero activation block (d = 0)
+    if k > 32:
+        x[:, 33] *= np.float32(50)
+    x = (x * np.float32(scale)).astype(np.float32)
+    return w, x
+
+
+def norms(orc, t, w, x):
+    """||w_row|| per row (exact dequantised values) and ||x|| per column."""
+    wn = np.array([orc.evaluate_row(t, w[r], np.zeros(x.shape[1], np.float32)).weight_norm for r in range(w.shape[0])])
+    xn = np.linalg.norm(x.astype(np.float64), axis=1)
+    return wn, xn
+
+
+@pytest.mark.parametrize("scale", [1.0, 1e5, 1e-5])
+def test_quantize_q8_1_bit_exact(orc, gpu, scale):
+    import p100_amd as P
+
+    rng = np.random.default_rng(1)
+    for K in (32, 256, 4096, 14336):
+        x = (rng.standard_normal((3, K)) * scale).astype(np.float32)
+        x[0, :32] = 0
+        x[1, 5] = -x[1, 5] * 50
+        a = P.quantize_q8_1(to_dev(x))
+        qs = a.qs.cpu().numpy()
+        ds = a.ds.cpu().numpy()
+        for c in range(3):
+            q, d, s = orc.prepare_q8_1(x[c])
+            assert (qs[c] == q).all(), (K, c)
+            assert (ds[c, :, 0].view(np.uint32) == d.view(np.uint32)).all()
+            assert (ds[c, :, 1].view(np.uint32) == s.view(np.uint32)).all()
+            assert (ds[c, :, 2] == q.astype(np.int64).reshape(-1, 32).sum(1)).all()
+
+
+def test_prepare_h16_bit_exact(orc, gpu):
+    import p100_amd as P
+
+    rng = np.random.default_rng(2)
+    for K in (32, 4096, 14336):
+        x = rng.standard_normal((2, K)).astype(np.float32)
+        x[0, :32] = 0
+        x[1, 40] *= 1000
+        a = P.prepare_h16(to_dev(x))
+        h = a.h.cpu().numpy().view(np.uint16)
+        meta = a.meta.cpu().numpy()
+        for c in range(2):
+            hh, sc, sm = orc.prepare_h16(x[c])
+            assert (h[c] == hh).all()
+            assert (meta[c, :, 0].view(np.uint32) == sc.view(np.uint32)).all()
+            assert (meta[c, :, 1].view(np.uint32) == sm.view(np.uint32)).all()
+
+
+def test_device_fp16_conversion_matches_oracle(orc, gpu):
+    """Every half value, every midpoint between neighbours and its two float neighbours (test_fp16.cpp:42-57),
+    overflow and underflow edges, and 1M random finite floats: device bits == oracle bits."""
+    import p100_amd as P
+
+    b = np.arange(0, 0x7C00, dtype=np.uint32)
+    v = np.frombuffer(b.astype(np.uint16).tobytes(), np.float16).astype(np.float32)
+    nxt = np.frombuffer((b + 1).astype(np.uint16).tobytes(), np.float16).astype(np.float32)
+    mid = ((v.astype(np.float64) + nxt) * 0.5).astype(np.float32)
+    xs = np.concatenate([v, mid, np.nextafter(mid, v), np.nextafter(mid, nxt),
+                         np.float32([65504, 65519.99, 65520, 70000, 3e38, 2.0 ** -25, 2.0 ** -24, 1e-40, 0.0])])
+    xs = np.concatenate([xs, -xs])
+    rnd = np.random.default_rng(3).integers(0, 2 ** 32, 1 << 20, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    xs = np.concatenate([xs, rnd[np.isfinite(rnd)], np.float32([np.inf, -np.inf])])
+    dev = P.round_to_fp16(to_dev(xs)).cpu().numpy().view(np.uint16)
+    want = np.frombuffer(orc.round_to_fp16(xs).astype(np.float16).tobytes(), np.uint16)
+    bad = np.nonzero(dev != want)[0]
+    assert bad.size == 0, [(float(xs[i]), hex(dev[i]), hex(want[i])) for i in bad[:8]]
+
+
+def check_matvec(orc, t, w, x, y, sums, mode):
+    """y [ncols, M] (and group sums) against the oracle: bit-exact sums, FP32 within the bars above."""
+    rows, k = w.shape[0], x.shape[1]
+    ref, ref_sums = (orc.mul_mat_vec(t, w, rows, k, x, mode=mode, want_sums=True) if mode == "q81"
+                     else (orc.mul_mat_vec(t, w, rows, k, x, mode=mode), None))
+    exact = orc.mul_mat_vec(t, w, rows, k, x, mode="exact").astype(np.float64)
+    wn, xn = norms(orc, t, w, x)
+    scale = np.outer(xn, wn)
+    if sums is not None:
+        assert (sums == ref_sums).all()
+    fin = np.isfinite(ref)
+    # Non-finite results (fp16 overflow of s at x1e5) are order independent: same class on both sides.
+    assert (np.isnan(y) == np.isnan(ref)).all() and (np.isposinf(y) == np.isposinf(ref)).all()
+    err_model = np.abs(y[fin].astype(np.float64) - ref[fin]) / np.where(scale[fin] > 0, scale[fin], 1)
+    assert err_model.max(initial=0) <= 1e-5, err_model.max()
+    fin_e = fin & np.isfinite(exact)
+    err_exact = np.abs(y[fin_e].astype(np.float64) - exact[fin_e]) / np.where(scale[fin_e] > 0, scale[fin_e], 1)
+    return err_model.max(initial=0), err_exact.max(initial=0)
+
+
+@pytest.mark.parametrize("tname", TYPES)
+def test_mmvq_parity(orc, gpu, tname):
+    import p100_amd as P
+
+    t = orc.TYPES[tname]
+    nb = orc.BLOCK[t][0]
+    worst = 0.0
+    for k in (nb, 2 * nb, 4096, 14336):
+        for ncols in range(1, 9):
+            w, x = make_case(orc, t, k, 17, ncols, seed=600602 + k * 10 + ncols)
+            y, sums = P.mul_mat_vec(t, to_dev(w), 17, k, to_dev(x), act="q8_1", group_sums=True)
+            em, ee = check_matvec(orc, t, w, x, y.cpu().numpy(), sums.cpu().numpy(), "q81")
+            assert ee <= 1e-3, (k, ncols, ee)
+            worst = max(worst, ee)
+            # The same result without the group-sum export, and through a prepared activation.
+            y2 = P.mul_mat_vec(t, to_dev(w), 17, k, to_dev(x), act="q8_1").cpu().numpy()
+            y3 = P.mul_mat_vec(t, to_dev(w), 17, k, P.quantize_q8_1(to_dev(x))).cpu().numpy()
+            assert (y2.view(np.uint32) == y.cpu().numpy().view(np.uint32)).all()
+            assert (y3.view(np.uint32) == y2.view(np.uint32)).all()
+    print(f"{tname} q81 worst |y-exact|/(|w||x|) = {worst:.3e}")
+
+
+@pytest.mark.parametrize("tname", TYPES)
+@pytest.mark.parametrize("scale", [1e5, 1e-5])
+def test_mmvq_activation_ranges(orc, gpu, tname, scale):
+    import p100_amd as P
+
+    t = orc.TYPES[tname]
+    for k in (4096,):
+        w, x = make_case(orc, t, k, 17, 2, seed=1500 + k, scale=scale)
+        y, sums = P.mul_mat_vec(t, to_dev(w), 17, k, to_dev(x), act="q8_1", group_sums=True)
+        check_matvec(orc, t, w, x, y.cpu().numpy(), sums.cpu().numpy(), "q81")
+
+
+@pytest.mark.parametrize("tname", TYPES)
+def test_mmvh_parity(orc, gpu, tname):
+    import p100_amd as P
+
+    t = orc.TYPES[tname]
+    nb = orc.BLOCK[t][0]
+    for k in (nb, 2 * nb, 4096, 14336):
+        for ncols in (1, 2, 3, 4, 8):
+            w, x = make_case(orc, t, k, 17, ncols, seed=700 + k + ncols)
+            y = P.mul_mat_vec(t, to_dev(w), 17, k, to_dev(x), act="h16").cpu().numpy()
+            em, ee = check_matvec(orc, t, w, x, y, None, "h16")
+            assert ee <= 1e-3, (k, ncols, ee)
+            y2 = P.mul_mat_vec(t, to_dev(w), 17, k, P.prepare_h16(to_dev(x))).cpu().numpy()
+            assert (y2.view(np.uint32) == y.view(np.uint32)).all()
+
+
+def test_h16_single_block_is_bit_exact(orc, gpu):
+    """One block per row: the fp16 chain and its flush have a single order, so GPU == model bit for bit."""
+    import p100_amd as P
+
+    for tname in TYPES:
+        t = orc.TYPES[tname]
+        nb = orc.BLOCK[t][0]
+        w, x = make_case(orc, t, nb, 33, 4, seed=42)
+        y = P.mul_mat_vec(t, to_dev(w), 33, nb, to_dev(x), act="h16").cpu().numpy()
+        ref = orc.mul_mat_vec(t, w, 33, nb, x, mode="h16")
+        if nb == 32:
+            assert (y.view(np.uint32) == ref.view(np.uint32)).all(), tname
+
+
+@pytest.mark.parametrize("tname", TYPES)
+def test_row_stride_and_large_m(orc, gpu, tname):
+    """Padded row stride (nb01 > row bytes), and enough rows to use every work-group shape."""
+    import p100_amd as P
+
+    t = orc.TYPES[tname]
+    for k, rows in ((4096, 1024), (256 if orc.BLOCK[t][0] == 256 else 96, 3000)):
+        w, x = make_case(orc, t, k, rows, 1, seed=rows + k)
+        rb = w.shape[1]
+        pad = np.zeros((rows, rb + 6), np.uint8)
+        pad[:, :rb] = w
+        y = P.mul_mat_vec(t, to_dev(pad), rows, k, to_dev(x), nb01=rb + 6).cpu().numpy()
+        ref = orc.mul_mat_vec(t, w, rows, k, x)
+        wn, xn = norms(orc, t, w, x)
+        assert (np.abs(y - ref) / np.outer(xn, wn)).max() <= 1e-5
+
+
+def test_invalid_arguments(gpu):
+    import p100_amd as P
+
+    torch = _torch()
+    w = torch.zeros(18 * 4, dtype=torch.uint8, device="cuda")
+    x = torch.zeros(32, dtype=torch.float32, device="cuda")
+    with pytest.raises(ValueError, match="multiple of the block size"):
+        P.mul_mat_vec("q4_K", w, 1, 32, x)
+    with pytest.raises(ValueError, match="ncols"):
+        P.mul_mat_vec("q4_0", w, 1, 32, torch.zeros((9, 32), device="cuda"))
+    with pytest.raises(ValueError, match="row stride"):
+        P.mul_mat_vec("q4_0", w, 1, 32, x, nb01=16)
+    with pytest.raises(P.P1XError):
+        P.mul_mat_vec(3, w, 1, 32, x)
