@@ -119,6 +119,14 @@ def _ptr(t):
     return None if t is None else C.c_void_p(t.data_ptr())
 
 
+def _params(p) -> AttnParams:
+    """Accepts AttnParams or any object with the same fields (e.g. the oracle's mirror of the struct)."""
+    if isinstance(p, AttnParams):
+        return p
+    return AttnParams(p.batch, p.n_head_q, p.n_head_kv, p.seq_q, p.seq_kv, p.d_qk, p.d_v, p.scale, p.softcap,
+                      bool(p.causal))
+
+
 def _stream(stream):
     import torch
 
@@ -182,7 +190,10 @@ def mul_mat_vec(wtype, w, M, K, x, act="q8_1", nb01=None, group_sums=False, out=
 
     lib = load()
     wtype = TYPES.get(wtype, wtype)
-    nb01 = row_bytes(wtype, K) if nb01 is None else nb01
+    if nb01 is None:
+        nb01 = row_bytes(wtype, K) if wtype in BLOCK else 0  # unknown types are rejected by the library
+    if group_sums and wtype not in GROUP:
+        raise P1XError(EUNSUPPORTED, f"unsupported weight type {wtype}")
     s = _stream(stream)
     if isinstance(x, Q81):
         ncols = x.qs.shape[0]
@@ -220,11 +231,12 @@ def mul_mat_vec_workspace(wtype, M, K, ncols, act="q8_1") -> int:
 def validate(p: AttnParams) -> str:
     """'' if p is valid, else p100::validate's reason string."""
     lib = load()
+    p = _params(p)
     return "" if lib.p1x_attn_validate(C.byref(p)) == OK else lib.p1x_last_error().decode()
 
 
 def flash_attn_decode_workspace(p: AttnParams) -> int:
-    return load().p1x_flash_attn_decode_workspace(C.byref(p))
+    return load().p1x_flash_attn_decode_workspace(C.byref(_params(p)))
 
 
 def flash_attn_decode(p: AttnParams, q, k, v, mask=None, strides: KVStrides | None = None, want_lse=True, out=None,
@@ -237,6 +249,7 @@ def flash_attn_decode(p: AttnParams, q, k, v, mask=None, strides: KVStrides | No
     import torch
 
     lib = load()
+    p = _params(p)
     why = validate(p)
     if why:
         raise ValueError(why)

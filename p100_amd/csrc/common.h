@@ -26,7 +26,8 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
     return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
-// Selector that extracts 4 consecutive bytes starting at byte offset `shift` (0 or 2) of {hi:lo}.
+// For a q4_0 / q8_0 block whose first byte is at byte `shift` (0 or 2) of the dword w[0]: the selector that
+// extracts 4 consecutive quant bytes from {w[i+1]:w[i]}, the quants starting 2 bytes (the fp16 d) after the block.
 __device__ __forceinline__ uint32_t slice_sel(uint32_t shift) { return shift ? 0x07060504u : 0x05040302u; }
 
 // GGUF q4_0 / q8_0 blocks sit at 2-byte alignment (18 / 34-byte strides). Both loaders read whole dwords
@@ -73,7 +74,7 @@ __device__ __forceinline__ void load_field(const uint8_t* p, uint32_t* out) {
         w[i + 3] = v.w;
     }
     w[N] = base[N];
-    const uint32_t sel = slice_sel(uint32_t(a & 2));
+    const uint32_t sel = (a & 2) ? 0x05040302u : 0x03020100u;  // the field starts at byte 2 or 0 of w[0]
 #pragma unroll
     for (int i = 0; i < N; ++i) out[i] = perm(w[i + 1], w[i], sel);
 }

@@ -8,24 +8,43 @@
 // Pass 1 (k_fa_split): one 256-thread work-group per (split of the KV range, KV head, group of NH query heads
 // sharing it, query row). D/8 lanes own one key row (8 fp16 per lane, one 16-byte load), so a wave loads
 // 64*16 consecutive bytes of K or V per instruction; the 256/(D/8) key groups of the work-group interleave
-// over the split's keys and each keeps its own online-softmax state (FP32 m, l, and an 8-wide slice of O for
-// each of the NH heads). Groups merge through LDS; the work-group writes one unnormalised partial
-// (O[D], max, sum) per head. Logits are kept in base 2 (scaled by log2 e) so exponentials are v_exp_f32.
+// over the split's keys, kKeys keys per group per step (all their K and V loads issued together), and each
+// group keeps its own online-softmax state (FP32 m, l, and an 8-wide slice of O for each of the NH heads).
+// Logits are kept in base 2 (scaled by log2 e) so exponentials are v_exp_f32. Groups merge through LDS; the
+// work-group writes one unnormalised partial (O[D], max, sum) per head.
 // Pass 2 (k_fa_combine): per query row, rebase the partials to their common max and divide once
 // (the combine of fattn-common.cuh:963-977 as modelled in attention_tiled_model.cpp:183-222).
 #include "common.h"
 #include "launch.h"
 
 namespace p1x {
-
-
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+constexpr int kKeys = 4;         // keys per group per step
+constexpr int kMaxSplits = 256;  // fa_split_plan never exceeds this
 
-__device__ __forceinline__ void load_h8(const __half* p, float* out) {
-    const uint4 v = *reinterpret_cast<const uint4*>(p);
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
+}
+// DPP controls: quad_perm(1,0,3,2) = xor 1, quad_perm(2,3,0,1) = xor 2, row_half_mirror, row_mirror.
+constexpr int kXor1 = 0xB1, kXor2 = 0x4E, kHalfMirror = 0x141, kMirror = 0x140;
+
+// Sum over the aligned group of W (8, 16 or 32) lanes that own one key row; every lane gets the total.
+template <int W>
+__device__ __forceinline__ float key_sum(float v) {
+    v += dpp_f<kXor1>(v);
+    v += dpp_f<kXor2>(v);
+    v += dpp_f<kHalfMirror>(v);
+    if constexpr (W >= 16) v += dpp_f<kMirror>(v);
+    if constexpr (W >= 32)  // xor 16 inside each 32-lane half: ds_swizzle bit mode, and 0x1f, xor 0x10
+        v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+    return v;
+}
+
+__device__ __forceinline__ void h8_to_f32(uint4 v, float* out) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -74,43 +93,70 @@ __global__ __launch_bounds__(256) void k_fa_split(FaArgs a) {
     const __half* vb = a.v + size_t(b) * a.v_batch + size_t(kvh) * a.v_head + 8 * l;
     const float* mrow = a.mask ? a.mask + size_t(i) * a.seq_kv : nullptr;
 
-    for (int j = j0 + g; j < j1; j += G) {
-        float kf[8], vf[8];
-        load_h8(kb + size_t(j) * a.k_row, kf);
-        load_h8(vb + size_t(j) * a.v_row, vf);
-        float x[NH];
+    for (int jb = j0 + g; jb < j1; jb += G * kKeys) {
+        // Branch-free batch: keys past j1 reload key jb (valid) and get logit -inf.
+        uint4 kr[kKeys], vr[kKeys];
+        bool ok[kKeys];
 #pragma unroll
-        for (int hh = 0; hh < NH; ++hh) {
-            float dot = 0.0f;
-#pragma unroll
-            for (int d = 0; d < 8; ++d) dot = fmaf(qr[hh][d], kf[d], dot);
-            x[hh] = group_sum(dot, LPK);
+        for (int u = 0; u < kKeys; ++u) {
+            const int j = jb + u * G;
+            ok[u] = j < j1;
+            const int jc = ok[u] ? j : jb;
+            kr[u] = *reinterpret_cast<const uint4*>(kb + size_t(jc) * a.k_row);
+            vr[u] = *reinterpret_cast<const uint4*>(vb + size_t(jc) * a.v_row);
         }
-        if (cap || mrow) {
-            const float add = mrow ? mrow[j] : 0.0f;
+        float x[kKeys][NH];
+#pragma unroll
+        for (int u = 0; u < kKeys; ++u) {
+            float kf[8];
+            h8_to_f32(kr[u], kf);
 #pragma unroll
             for (int hh = 0; hh < NH; ++hh) {
-                float t = x[hh];
-                if (cap) t = (a.softcap * tanhf(t / a.softcap) + add) * kLog2e;
-                else t = t + add * kLog2e;
-                x[hh] = t;
+                float dot = 0.0f;
+#pragma unroll
+                for (int d = 0; d < 8; ++d) dot = fmaf(qr[hh][d], kf[d], dot);
+                x[u][hh] = key_sum<LPK>(dot);
             }
+            if (cap || mrow) {
+                const float add = (mrow && ok[u]) ? mrow[jb + u * G] : 0.0f;
+#pragma unroll
+                for (int hh = 0; hh < NH; ++hh)
+                    x[u][hh] = cap ? (a.softcap * tanhf(x[u][hh] / a.softcap) + add) * kLog2e : x[u][hh] + add * kLog2e;
+            }
+#pragma unroll
+            for (int hh = 0; hh < NH; ++hh) x[u][hh] = ok[u] ? x[u][hh] : -INFINITY;
         }
+        float vf[kKeys][8];
+#pragma unroll
+        for (int u = 0; u < kKeys; ++u) h8_to_f32(vr[u], vf[u]);
 #pragma unroll
         for (int hh = 0; hh < NH; ++hh) {
-            const float mn = fmaxf(m[hh], x[hh]);
+            float tmax = x[0][hh];
+#pragma unroll
+            for (int u = 1; u < kKeys; ++u) tmax = fmaxf(tmax, x[u][hh]);
+            const float mn = fmaxf(m[hh], tmax);
             if (mn == -INFINITY) continue;  // nothing visible yet for this state
             const float alpha = exp2f(m[hh] - mn);
-            const float p = exp2f(x[hh] - mn);
-            s[hh] = fmaf(s[hh], alpha, p);
+            float p[kKeys], psum = 0.0f;
 #pragma unroll
-            for (int d = 0; d < 8; ++d) o[hh][d] = fmaf(o[hh][d], alpha, p * vf[d]);
+            for (int u = 0; u < kKeys; ++u) {
+                p[u] = exp2f(x[u][hh] - mn);
+                psum += p[u];
+            }
+            s[hh] = fmaf(s[hh], alpha, psum);
+#pragma unroll
+            for (int d = 0; d < 8; ++d) {
+                float t = o[hh][d] * alpha;
+#pragma unroll
+                for (int u = 0; u < kKeys; ++u) t = fmaf(p[u], vf[u][d], t);
+                o[hh][d] = t;
+            }
             m[hh] = mn;
         }
     }
 
-    // Merge the G groups: LDS holds each group's (m, s) per head and its O slices.
-    __shared__ float sm[G][NH], ss[G][NH];
+    // Merge the G groups through LDS: per head, weights 2^(m_g - M) once, then O columns.
+    __shared__ float sm[G][NH], ss[G][NH], wt[G][NH], hmax[NH], hden[NH];
     __shared__ float so[G][NH][D];
 #pragma unroll
     for (int hh = 0; hh < NH; ++hh) {
@@ -122,50 +168,84 @@ __global__ __launch_bounds__(256) void k_fa_split(FaArgs a) {
         for (int d = 0; d < 8; ++d) so[g][hh][8 * l + d] = o[hh][d];
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < NH * D; idx += 256) {
-        const int hh = idx / D, d = idx % D;
+    if (threadIdx.x < NH) {
+        const int hh = threadIdx.x;
         float mx = -INFINITY;
         for (int gg = 0; gg < G; ++gg) mx = fmaxf(mx, sm[gg][hh]);
-        float num = 0.0f, den = 0.0f;
-        if (mx != -INFINITY) {
-            for (int gg = 0; gg < G; ++gg) {
-                if (ss[gg][hh] == 0.0f) continue;
-                const float w = exp2f(sm[gg][hh] - mx);
-                num = fmaf(w, so[gg][hh][d], num);
-                den = fmaf(w, ss[gg][hh], den);
-            }
+        float den = 0.0f;
+        for (int gg = 0; gg < G; ++gg) {
+            const float w = (ss[gg][hh] == 0.0f || mx == -INFINITY) ? 0.0f : exp2f(sm[gg][hh] - mx);
+            wt[gg][hh] = w;
+            den = fmaf(w, ss[gg][hh], den);
         }
+        hmax[hh] = mx;
+        hden[hh] = den;
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < NH * D; idx += 256) {
+        const int hh = idx / D, d = idx % D;
+        float num = 0.0f;
+#pragma unroll 8
+        for (int gg = 0; gg < G; ++gg) num = fmaf(wt[gg][hh], so[gg][hh][d], num);
         const size_t row = (size_t(b) * a.hq + h0 + hh) * a.seq_q + i;
         float* pp = a.part + (row * a.splits + split) * (D + 2);
         pp[d] = num;
         if (d == 0) {
-            pp[D] = mx;
-            pp[D + 1] = den;
+            pp[D] = hmax[hh];
+            pp[D + 1] = hden[hh];
         }
     }
 }
 
-// One work-group of D threads per query row: thread d owns output column d.
+// One 256-thread work-group per query row. Thread (d = tid % D, part = tid / D) sums splits part, part + P, ...
 template <int D>
-__global__ __launch_bounds__(D) void k_fa_combine(const float* __restrict__ part, int splits, float* __restrict__ o,
-                                                  float* __restrict__ lse) {
+__global__ __launch_bounds__(256) void k_fa_combine(const float* __restrict__ part, int splits, float* __restrict__ o,
+                                                    float* __restrict__ lse) {
+    constexpr int P = 256 / D;
+    __shared__ float w[kMaxSplits];
+    __shared__ float red[256];
+    __shared__ float stat[2];
     const size_t row = blockIdx.x;
-    const int d = threadIdx.x;
+    const int tid = threadIdx.x;
     const float* p = part + row * splits * (D + 2);
     float mx = -INFINITY;
-    for (int sp = 0; sp < splits; ++sp) mx = fmaxf(mx, p[sp * (D + 2) + D]);
-    float num = 0.0f, den = 0.0f;
-    if (mx != -INFINITY) {
-        for (int sp = 0; sp < splits; ++sp) {
-            const float* q = p + sp * (D + 2);
-            if (q[D + 1] == 0.0f) continue;
-            const float w = exp2f(q[D] - mx);
-            num = fmaf(w, q[d], num);
-            den = fmaf(w, q[D + 1], den);
-        }
+    for (int sp = tid; sp < splits; sp += 256) mx = fmaxf(mx, p[sp * (D + 2) + D]);
+    red[tid] = mx;
+    __syncthreads();
+    for (int off = 128; off > 0; off >>= 1) {
+        if (tid < off) red[tid] = fmaxf(red[tid], red[tid + off]);
+        __syncthreads();
     }
-    o[row * D + d] = den == 0.0f ? 0.0f : num / den;
-    if (lse && d == 0) lse[row] = den == 0.0f ? -INFINITY : (mx + log2f(den)) * kLn2;
+    mx = red[0];
+    __syncthreads();
+    float den = 0.0f;
+    for (int sp = tid; sp < splits; sp += 256) {
+        const float l = p[sp * (D + 2) + D + 1];
+        const float wv = (l == 0.0f || mx == -INFINITY) ? 0.0f : exp2f(p[sp * (D + 2) + D] - mx);
+        w[sp] = wv;
+        den = fmaf(wv, l, den);
+    }
+    red[tid] = den;
+    __syncthreads();
+    for (int off = 128; off > 0; off >>= 1) {
+        if (tid < off) red[tid] += red[tid + off];
+        __syncthreads();
+    }
+    if (tid == 0) stat[0] = red[0];
+    __syncthreads();
+    den = stat[0];
+    const int d = tid % D, pt = tid / D;
+    float num = 0.0f;
+#pragma unroll 4
+    for (int sp = pt; sp < splits; sp += P) num = fmaf(w[sp], p[sp * (D + 2) + d], num);
+    __syncthreads();
+    red[tid] = num;
+    __syncthreads();
+    if (pt == 0) {
+        for (int q = 1; q < P; ++q) num += red[q * D + d];
+        o[row * D + d] = den == 0.0f ? 0.0f : num / den;
+        if (lse && d == 0) lse[row] = den == 0.0f ? -INFINITY : (mx + log2f(den)) * kLn2;
+    }
 }
 
 template <int D, int NH>
@@ -186,7 +266,7 @@ hipError_t launch_d(FaArgs a, int batch, int nh, float* o, float* lse, hipStream
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const dim3 grid(unsigned(size_t(batch) * a.hq * a.seq_q));
-    hipLaunchKernelGGL((k_fa_combine<D>), grid, dim3(D), 0, stream, a.part, a.splits, o, lse);
+    hipLaunchKernelGGL((k_fa_combine<D>), grid, dim3(256), 0, stream, a.part, a.splits, o, lse);
     return hipGetLastError();
 }
 
@@ -200,7 +280,7 @@ int fa_heads_per_wg(int hq, int hkv) {
     return 1;
 }
 
-// KV split: aim for ~1024 work-groups in pass 1, at least 64 keys per split, at most 256 splits.
+// KV split: aim for ~1024 work-groups in pass 1, at least 64 keys per split, at most kMaxSplits splits.
 void fa_split_plan(int batch, int hq, int hkv, int seq_q, int seq_kv, int& splits, int& chunk) {
     const int nh = fa_heads_per_wg(hq, hkv);
     const long wgs_per_split = long(batch) * hkv * (hq / hkv / nh) * seq_q;
@@ -208,7 +288,7 @@ void fa_split_plan(int batch, int hq, int hkv, int seq_q, int seq_kv, int& split
     const long max_by_len = (seq_kv + 63) / 64;
     want = want < 1 ? 1 : want;
     want = want > max_by_len ? max_by_len : want;
-    want = want > 256 ? 256 : want;
+    want = want > kMaxSplits ? kMaxSplits : want;
     chunk = int((seq_kv + want - 1) / want);
     chunk = (chunk + 15) / 16 * 16;
     splits = (seq_kv + chunk - 1) / chunk;

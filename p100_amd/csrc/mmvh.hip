@@ -17,6 +17,12 @@
 namespace p1x {
 namespace {
 
+// Units per thread per step: as many as registers allow without spilling (more columns, fewer units).
+template <int TYPE, int B>
+constexpr int batch() {
+    return B == 1 ? (TYPE == Q6_K || TYPE == Q4_K ? 2 : 4) : (B <= 2 && TYPE != Q6_K ? 2 : 1);
+}
+
 struct H16 {
     const __half2* h;    // [B][K/2]
     const float2* meta;  // [B][K/32]
@@ -131,38 +137,49 @@ __global__ __launch_bounds__(256) void k_mmvh(const uint8_t* __restrict__ w, int
     float acc[B];
 #pragma unroll
     for (int c = 0; c < B; ++c) acc[c] = 0.0f;
-    if (m < M) {
+    if (m < M && t < units) {
         const uint8_t* row = w + size_t(m) * nb01;
-        for (int u = t; u < units; u += T) {
-            const Unpacked q = unpack<TYPE>(row, u);
+        // kBatch units per step with branch-free bodies (a unit past the row end is clamped to a valid one and
+        // its result dropped by a select), so the loads of the batch are in flight together.
+        constexpr int kBatch = batch<TYPE, B>();
+        for (int u0 = t; u0 < units; u0 += kBatch * T) {
 #pragma unroll
-            for (int c = 0; c < B; ++c) {
-                const uint4* hp = reinterpret_cast<const uint4*>(h + size_t(c) * (K / 2) + size_t(u) * 16);
-                const float2 md = meta[size_t(c) * (K / 32) + u];
-                __half2 x[16];
+            for (int bi = 0; bi < kBatch; ++bi) {
+                const int uu = u0 + bi * T;
+                const bool ok = uu < units;
+                const int u = ok ? uu : u0;
+                const Unpacked q = unpack<TYPE>(row, u);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint4 v = hp[i];
-                    x[4 * i] = bits_h2(v.x);
-                    x[4 * i + 1] = bits_h2(v.y);
-                    x[4 * i + 2] = bits_h2(v.z);
-                    x[4 * i + 3] = bits_h2(v.w);
-                }
-                if constexpr (TYPE == Q6_K) {
+                for (int c = 0; c < B; ++c) {
+                    const uint4* hp = reinterpret_cast<const uint4*>(h + size_t(c) * (K / 2) + size_t(u) * 16);
+                    const float2 md = meta[size_t(c) * (K / 32) + u];
+                    __half2 x[16];
 #pragma unroll
-                    for (int g = 0; g < 2; ++g) {
+                    for (int i = 0; i < 4; ++i) {
+                        const uint4 v = hp[i];
+                        x[4 * i] = bits_h2(v.x);
+                        x[4 * i + 1] = bits_h2(v.y);
+                        x[4 * i + 2] = bits_h2(v.z);
+                        x[4 * i + 3] = bits_h2(v.w);
+                    }
+                    float r = acc[c];
+                    if constexpr (TYPE == Q6_K) {
+#pragma unroll
+                        for (int g = 0; g < 2; ++g) {
+                            __half2 s = __float2half2_rn(0.0f);
+#pragma unroll
+                            for (int j = 8 * g; j < 8 * g + 8; ++j) s = __hfma2(q.q[j], x[j], s);
+                            const float ds = (g ? q.d1 : q.d0) * md.x;
+                            r += (__low2float(s) + __high2float(s)) * ds;
+                        }
+                    } else {
                         __half2 s = __float2half2_rn(0.0f);
 #pragma unroll
-                        for (int j = 8 * g; j < 8 * g + 8; ++j) s = __hfma2(q.q[j], x[j], s);
-                        const float ds = (g ? q.d1 : q.d0) * md.x;
-                        acc[c] += (__low2float(s) + __high2float(s)) * ds;
+                        for (int j = 0; j < 16; ++j) s = __hfma2(q.q[j], x[j], s);
+                        r += (__low2float(s) + __high2float(s)) * (q.d0 * md.x);
+                        if constexpr (TYPE == Q4_K) r -= (q.m * md.x) * md.y;
                     }
-                } else {
-                    __half2 s = __float2half2_rn(0.0f);
-#pragma unroll
-                    for (int j = 0; j < 16; ++j) s = __hfma2(q.q[j], x[j], s);
-                    acc[c] += (__low2float(s) + __high2float(s)) * (q.d0 * md.x);
-                    if constexpr (TYPE == Q4_K) acc[c] -= (q.m * md.x) * md.y;
+                    acc[c] = ok ? r : acc[c];
                 }
             }
         }

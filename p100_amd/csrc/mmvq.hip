@@ -8,6 +8,8 @@
 // Work split: a 256-thread work-group owns R = 256/T consecutive rows; the T threads of a row stride over the
 // row's "units" (a q4_0 / q8_0 block, a q4_K pair of 32-element sub-blocks, a q6_K 32-element sub-block),
 // so adjacent lanes read adjacent blocks and one wave load instruction covers a contiguous stretch of a row.
+// Each thread takes a batch of units per step with branch-free bodies (a unit past the row end is clamped to a
+// valid one and its result dropped by a select), so the loads of the whole batch are in flight together.
 // A unit's weights are decoded once and reused for all B activation columns. Partial sums are reduced across
 // the T threads (xor shuffles inside the wave, LDS across waves).
 #include "common.h"
@@ -17,6 +19,12 @@ namespace p1x {
 namespace {
 
 constexpr uint32_t kLo = 0x0F0F0F0Fu;
+
+// Units per thread per step: as many as registers allow without spilling (more columns, fewer units).
+template <int TYPE, int B>
+constexpr int batch() {
+    return B <= 2 ? (TYPE == Q4_K && B == 2 ? 2 : 4) : (B <= 4 ? 2 : 1);
+}
 
 struct Act {
     const int8_t* qs;  // [B][K]
@@ -31,45 +39,51 @@ __device__ __forceinline__ void load_act(const Act& a, int c, int blk, int4& lo,
     d = a.ds[size_t(c) * (a.K / 32) + blk];
 }
 
+__device__ __forceinline__ int dot8(const uint32_t* w, int4 x0, int4 x1) {
+    int s = dot4(int(w[0]), x0.x, 0);
+    s = dot4(int(w[1]), x0.y, s);
+    s = dot4(int(w[2]), x0.z, s);
+    s = dot4(int(w[3]), x0.w, s);
+    s = dot4(int(w[4]), x1.x, s);
+    s = dot4(int(w[5]), x1.y, s);
+    s = dot4(int(w[6]), x1.z, s);
+    return dot4(int(w[7]), x1.w, s);
+}
+
 // ---------------------------------------------------------------- per-type units
+// Each unit adds its contribution to acc[c] (only when ok) and, with SUMS, stores its int32 group sums.
+
 // q4_0: 18-byte block {fp16 d, qs[16]}; element j < 16 is the low nibble of qs[j], j + 16 the high nibble.
 // Reference q81: sum over both calls of fma(d, fma(float(dot), d8, -4 s8), acc) with dot over the unsigned
 // nibbles (qmv_model.cpp:151-160); one call per block here: fma(d, fma(float(dot), d8, -8 s8), acc).
 template <int B, bool SUMS>
-__device__ __forceinline__ void unit_q4_0(const uint8_t* row, int u, const Act& a, float* acc, int32_t* gs,
-                                          size_t gs_col, int gs_row_len) {
+__device__ __forceinline__ void unit_q4_0(const uint8_t* row, int u, bool ok, const Act& a, float* acc, int32_t* gs,
+                                          size_t gcol) {
     uint32_t q[4], dbits;
     load_q4_0_block(row + size_t(u) * 18, q, dbits);
     const float d = half_bits_to_float(dbits);
-    uint32_t lo[4], hi[4];
+    uint32_t n[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        lo[j] = q[j] & kLo;
-        hi[j] = (q[j] >> 4) & kLo;
+        n[j] = q[j] & kLo;
+        n[4 + j] = (q[j] >> 4) & kLo;
     }
 #pragma unroll
     for (int c = 0; c < B; ++c) {
         int4 x0, x1;
         float4 dd;
         load_act(a, c, u, x0, x1, dd);
-        int dot = dot4(int(lo[0]), x0.x, 0);
-        dot = dot4(int(lo[1]), x0.y, dot);
-        dot = dot4(int(lo[2]), x0.z, dot);
-        dot = dot4(int(lo[3]), x0.w, dot);
-        dot = dot4(int(hi[0]), x1.x, dot);
-        dot = dot4(int(hi[1]), x1.y, dot);
-        dot = dot4(int(hi[2]), x1.z, dot);
-        dot = dot4(int(hi[3]), x1.w, dot);
-        acc[c] = fmaf(d, fmaf(float(dot), dd.x, -8.0f * dd.y), acc[c]);
-        if constexpr (SUMS) gs[gs_col * c + u] = dot;
+        const int dot = dot8(n, x0, x1);
+        const float v = fmaf(d, fmaf(float(dot), dd.x, -8.0f * dd.y), acc[c]);
+        acc[c] = ok ? v : acc[c];
+        if (SUMS && ok) gs[gcol * c + u] = dot;
     }
-    (void)gs_row_len;
 }
 
 // q8_0: 34-byte block {fp16 d, int8 qs[32]}; reference: fma(d * d8, float(dot), acc) (qmv_model.cpp:161).
 template <int B, bool SUMS>
-__device__ __forceinline__ void unit_q8_0(const uint8_t* row, int u, const Act& a, float* acc, int32_t* gs,
-                                          size_t gs_col, int gs_row_len) {
+__device__ __forceinline__ void unit_q8_0(const uint8_t* row, int u, bool ok, const Act& a, float* acc, int32_t* gs,
+                                          size_t gcol) {
     uint32_t q[8], dbits;
     load_q8_0_block(row + size_t(u) * 34, q, dbits);
     const float d = half_bits_to_float(dbits);
@@ -78,18 +92,11 @@ __device__ __forceinline__ void unit_q8_0(const uint8_t* row, int u, const Act& 
         int4 x0, x1;
         float4 dd;
         load_act(a, c, u, x0, x1, dd);
-        int dot = dot4(int(q[0]), x0.x, 0);
-        dot = dot4(int(q[1]), x0.y, dot);
-        dot = dot4(int(q[2]), x0.z, dot);
-        dot = dot4(int(q[3]), x0.w, dot);
-        dot = dot4(int(q[4]), x1.x, dot);
-        dot = dot4(int(q[5]), x1.y, dot);
-        dot = dot4(int(q[6]), x1.z, dot);
-        dot = dot4(int(q[7]), x1.w, dot);
-        acc[c] = fmaf(d * dd.x, float(dot), acc[c]);
-        if constexpr (SUMS) gs[gs_col * c + u] = dot;
+        const int dot = dot8(q, x0, x1);
+        const float v = fmaf(d * dd.x, float(dot), acc[c]);
+        acc[c] = ok ? v : acc[c];
+        if (SUMS && ok) gs[gcol * c + u] = dot;
     }
-    (void)gs_row_len;
 }
 
 // q4_K: 144-byte super-block {fp16 d, fp16 dmin, scales[12], qs[128]}; a unit is the pair of sub-blocks
@@ -108,8 +115,8 @@ __device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t
 }
 
 template <int B, bool SUMS>
-__device__ __forceinline__ void unit_q4_K(const uint8_t* row, int u, const Act& a, float* acc, int32_t* gs,
-                                          size_t gs_col, int gs_row_len) {
+__device__ __forceinline__ void unit_q4_K(const uint8_t* row, int u, bool ok, const Act& a, float* acc, int32_t* gs,
+                                          size_t gcol) {
     const int blk = u >> 2, g = u & 3;
     const uint32_t* p = reinterpret_cast<const uint32_t*>(row + size_t(blk) * 144);  // 4-byte aligned
     const U32x4 hdr = ld_u32x4(p);
@@ -132,31 +139,17 @@ __device__ __forceinline__ void unit_q4_K(const uint8_t* row, int u, const Act& 
         float4 dx, dy;
         load_act(a, c, ab, x0, x1, dx);
         load_act(a, c, ab + 1, y0, y1, dy);
-        int d0 = dot4(int(lo[0]), x0.x, 0);
-        d0 = dot4(int(lo[1]), x0.y, d0);
-        d0 = dot4(int(lo[2]), x0.z, d0);
-        d0 = dot4(int(lo[3]), x0.w, d0);
-        d0 = dot4(int(lo[4]), x1.x, d0);
-        d0 = dot4(int(lo[5]), x1.y, d0);
-        d0 = dot4(int(lo[6]), x1.z, d0);
-        d0 = dot4(int(lo[7]), x1.w, d0);
-        int d1 = dot4(int(hi[0]), y0.x, 0);
-        d1 = dot4(int(hi[1]), y0.y, d1);
-        d1 = dot4(int(hi[2]), y0.z, d1);
-        d1 = dot4(int(hi[3]), y0.w, d1);
-        d1 = dot4(int(hi[4]), y1.x, d1);
-        d1 = dot4(int(hi[5]), y1.y, d1);
-        d1 = dot4(int(hi[6]), y1.z, d1);
-        d1 = dot4(int(hi[7]), y1.w, d1);
+        const int d0 = dot8(lo, x0, x1);
+        const int d1 = dot8(hi, y0, y1);
         const float sd = fmaf(dy.x, float(d1 * sc1), dx.x * float(d0 * sc0));
         const float sm = fmaf(dy.x, dy.z * float(mn1), dx.x * (dx.z * float(mn0)));
-        acc[c] += fmaf(d, sd, -dmin * sm);
-        if constexpr (SUMS) {
-            gs[gs_col * c + 2 * u] = d0;
-            gs[gs_col * c + 2 * u + 1] = d1;
+        const float v = acc[c] + fmaf(d, sd, -dmin * sm);
+        acc[c] = ok ? v : acc[c];
+        if (SUMS && ok) {
+            gs[gcol * c + 2 * u] = d0;
+            gs[gcol * c + 2 * u + 1] = d1;
         }
     }
-    (void)gs_row_len;
 }
 
 // q6_K: 210-byte super-block {ql[128], qh[64], int8 scales[16], fp16 d}; a unit is one 32-element sub-block s.
@@ -164,8 +157,8 @@ __device__ __forceinline__ void unit_q4_K(const uint8_t* row, int u, const Act& 
 // from qh[(s/4)*32 + i] >> 2*(s%4); q6 = value - 32; scale per 16 = scales[2s + i/16] (ggml dequantize_row_q6_K).
 // Reference arithmetic (vec_dot_q6_K_q8_1): d * sum(d8 * dot16 * sc) with exact int32 dot16 per 16 elements.
 template <int B, bool SUMS>
-__device__ __forceinline__ void unit_q6_K(const uint8_t* row, int u, const Act& a, float* acc, int32_t* gs,
-                                          size_t gs_col, int gs_row_len) {
+__device__ __forceinline__ void unit_q6_K(const uint8_t* row, int u, bool ok, const Act& a, float* acc, int32_t* gs,
+                                          size_t gcol) {
     const int blk = u >> 3, s = u & 7;
     const uint8_t* p = row + size_t(blk) * 210;
     uint32_t ql[8], qh[8];
@@ -175,32 +168,32 @@ __device__ __forceinline__ void unit_q6_K(const uint8_t* row, int u, const Act& 
     const int sc0 = int(int8_t(sw & 255)), sc1 = int(int8_t((sw >> 8) & 255));
     const float d = half_bits_to_float(load_u16(p + 208));
     const int nsh = (s & 2) ? 4 : 0, hsh = 2 * (s & 3);
-    int32_t q6[8];
+    uint32_t q6[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const uint32_t v = ((ql[j] >> nsh) & kLo) | (((qh[j] >> hsh) & 0x03030303u) << 4);  // 0..63 per byte
-        q6[j] = int32_t((((v | 0x80808080u) - 0x20202020u)) ^ 0x80808080u);               // v - 32 per byte
+        q6[j] = ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u;                             // v - 32 per byte
     }
 #pragma unroll
     for (int c = 0; c < B; ++c) {
         int4 x0, x1;
         float4 dd;
         load_act(a, c, u, x0, x1, dd);
-        int g0 = dot4(q6[0], x0.x, 0);
-        g0 = dot4(q6[1], x0.y, g0);
-        g0 = dot4(q6[2], x0.z, g0);
-        g0 = dot4(q6[3], x0.w, g0);
-        int g1 = dot4(q6[4], x1.x, 0);
-        g1 = dot4(q6[5], x1.y, g1);
-        g1 = dot4(q6[6], x1.z, g1);
-        g1 = dot4(q6[7], x1.w, g1);
-        acc[c] = fmaf(d * dd.x, float(g0 * sc0 + g1 * sc1), acc[c]);
-        if constexpr (SUMS) {
-            gs[gs_col * c + 2 * u] = g0;
-            gs[gs_col * c + 2 * u + 1] = g1;
+        int g0 = dot4(int(q6[0]), x0.x, 0);
+        g0 = dot4(int(q6[1]), x0.y, g0);
+        g0 = dot4(int(q6[2]), x0.z, g0);
+        g0 = dot4(int(q6[3]), x0.w, g0);
+        int g1 = dot4(int(q6[4]), x1.x, 0);
+        g1 = dot4(int(q6[5]), x1.y, g1);
+        g1 = dot4(int(q6[6]), x1.z, g1);
+        g1 = dot4(int(q6[7]), x1.w, g1);
+        const float v = fmaf(d * dd.x, float(g0 * sc0 + g1 * sc1), acc[c]);
+        acc[c] = ok ? v : acc[c];
+        if (SUMS && ok) {
+            gs[gcol * c + 2 * u] = g0;
+            gs[gcol * c + 2 * u + 1] = g1;
         }
     }
-    (void)gs_row_len;
 }
 
 template <int TYPE>
@@ -208,6 +201,15 @@ struct Unit {
     static constexpr int elems = TYPE == Q4_K ? 64 : 32;
     static constexpr int groups = TYPE == Q4_0 || TYPE == Q8_0 ? 1 : 2;  // int32 sums per unit
 };
+
+template <int TYPE, int B, bool SUMS>
+__device__ __forceinline__ void unit(const uint8_t* row, int u, bool ok, const Act& a, float* acc, int32_t* gs,
+                                     size_t gcol) {
+    if constexpr (TYPE == Q4_0) unit_q4_0<B, SUMS>(row, u, ok, a, acc, gs, gcol);
+    if constexpr (TYPE == Q8_0) unit_q8_0<B, SUMS>(row, u, ok, a, acc, gs, gcol);
+    if constexpr (TYPE == Q4_K) unit_q4_K<B, SUMS>(row, u, ok, a, acc, gs, gcol);
+    if constexpr (TYPE == Q6_K) unit_q6_K<B, SUMS>(row, u, ok, a, acc, gs, gcol);
+}
 
 template <int TYPE, int B, bool SUMS>
 __global__ __launch_bounds__(256) void k_mmvq(const uint8_t* __restrict__ w, int64_t nb01, int M, int K, int tlog2,
@@ -221,16 +223,19 @@ __global__ __launch_bounds__(256) void k_mmvq(const uint8_t* __restrict__ w, int
     float acc[B];
 #pragma unroll
     for (int c = 0; c < B; ++c) acc[c] = 0.0f;
-    if (m < M) {
+    if (m < M && t < units) {
         const uint8_t* row = w + size_t(m) * nb01;
         const int glen = units * Unit<TYPE>::groups;           // int32 sums per row
         int32_t* grow = SUMS ? gs + size_t(m) * glen : nullptr;  // column c adds c * M * glen
         const size_t gcol = size_t(M) * glen;
-        for (int u = t; u < units; u += T) {
-            if constexpr (TYPE == Q4_0) unit_q4_0<B, SUMS>(row, u, a, acc, grow, gcol, glen);
-            if constexpr (TYPE == Q8_0) unit_q8_0<B, SUMS>(row, u, a, acc, grow, gcol, glen);
-            if constexpr (TYPE == Q4_K) unit_q4_K<B, SUMS>(row, u, a, acc, grow, gcol, glen);
-            if constexpr (TYPE == Q6_K) unit_q6_K<B, SUMS>(row, u, a, acc, grow, gcol, glen);
+        constexpr int kBatch = batch<TYPE, B>();
+        for (int u0 = t; u0 < units; u0 += kBatch * T) {
+#pragma unroll
+            for (int i = 0; i < kBatch; ++i) {
+                const int u = u0 + i * T;
+                const bool ok = u < units;
+                unit<TYPE, B, SUMS>(row, ok ? u : u0, ok, a, acc, grow, gcol);
+            }
         }
     }
     // Reduce over the T threads of each row.
@@ -295,9 +300,9 @@ hipError_t launch_type(int B, const uint8_t* w, int64_t nb01, int M, int K, int 
 // Threads per row: enough work-groups to cover the 256 CUs several times, and at least one unit per thread.
 int mmvq_threads_log2(int type, int M, int K) {
     const int units = K / (type == Q4_K ? 64 : 32);
-    int tl = 6;                                            // one wave per row
+    int tl = 6;                                                             // one wave per row
     while (tl < 8 && (M >> (8 - tl)) < 1024 && units >= (2 << tl)) ++tl;  // few rows: more threads per row
-    while (tl > 5 && units < (1 << tl)) --tl;              // short rows: fewer threads per row
+    while (tl > 5 && units < (1 << tl)) --tl;                               // short rows: fewer threads per row
     return tl;
 }
 
