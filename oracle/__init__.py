@@ -1,7 +1,7 @@
 """ctypes access to the CPU oracle (liboracle.so) and the reference build (_ref/libp100_ref.so).
 
 TEST INFRASTRUCTURE ONLY. Only tests/, ``__graft_entry__.smoke()`` and bench.py's cpu_baseline leg
-may import this package, and only as the checker (or as the timed CPU baseline). The product path in
+may import this package, and only to check results (or as the timed CPU baseline). The product path in
 ``p100_amd`` never does. Function-by-function reference citations are in ``oracle/oracle.h``.
 """
 from __future__ import annotations

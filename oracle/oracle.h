@@ -3,8 +3,8 @@
  *
  * This library restates, in plain C++17 built with -O2 -ffp-contract=off, the numerics contract
  * of the reference's CPU models so that the HIP kernels in p100_amd/ can be checked against it.
- * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it, and only as
- * the checker (or, for cpu_baseline, as the timed CPU restatement). The product path never calls it.
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it, and only to check
+ * results against (or, for cpu_baseline, as the timed CPU restatement). The product path never calls it.
  *
  * Functions and the reference code each one follows (paths relative to the reference repo):
  *   orc_round_to_fp16_f32   src/reference/attention_reference.cpp:34-85

@@ -5,13 +5,14 @@
 // The FP32 scale arithmetic per group follows the same formulas (FMA where the reference fuses), with one
 // call per group instead of ggml's 2-4 partial calls, so FP32 results agree to rounding, not bit for bit.
 //
-// Work split: a 256-thread work-group owns R = 256/T consecutive rows; the T threads of a row stride over the
-// row's "units" (a q4_0 / q8_0 block, a q4_K pair of 32-element sub-blocks, a q6_K 32-element sub-block),
-// so adjacent lanes read adjacent blocks and one wave load instruction covers a contiguous stretch of a row.
-// Each thread takes a batch of units per step with branch-free bodies (a unit past the row end is clamped to a
-// valid one and its result dropped by a select), so the loads of the whole batch are in flight together.
-// A unit's weights are decoded once and reused for all B activation columns. Partial sums are reduced across
-// the T threads (xor shuffles inside the wave, LDS across waves).
+// Work split (wave64 row ownership): each wave owns RW consecutive rows. Its 64 lanes stride over the row's
+// "units" (a q4_0 / q8_0 block, a q4_K pair of 32-element sub-blocks, a q6_K 32-element sub-block), UB units per
+// lane per pass over K, so one wave load instruction covers a contiguous stretch of a row. A pass first loads
+// the lane's Q8_1 activation blocks into registers, then the weights of all RW rows x UB units at once (every
+// load of the pass in flight together), then computes: the activation is read once per wave and reused by
+// RW rows and B columns reuse each decoded weight. Units past the row end are clamped to a valid unit and their
+// result dropped by a select, so the bodies stay branch-free. Lane partials are reduced with DPP and two
+// cross-row swizzles; four independent waves form a 256-thread work-group.
 #include "common.h"
 #include "launch.h"
 
@@ -20,23 +21,14 @@ namespace {
 
 constexpr uint32_t kLo = 0x0F0F0F0Fu;
 
-// Units per thread per step: as many as registers allow without spilling (more columns, fewer units).
-template <int TYPE, int B>
-constexpr int batch() {
-    return B <= 2 ? (TYPE == Q4_K && B == 2 ? 2 : 4) : (B <= 4 ? 2 : 1);
-}
-
-struct Act {
-    const int8_t* qs;  // [B][K]
-    const float4* ds;  // [B][K/32]: d, s, isum, 0
-    int K;
+struct ActBlock {  // one 32-element Q8_1 block: q[0..15], q[16..31], {d, s, isum, 0}
+    int4 lo, hi;
+    float4 ds;
 };
 
-__device__ __forceinline__ void load_act(const Act& a, int c, int blk, int4& lo, int4& hi, float4& d) {
-    const int4* p = reinterpret_cast<const int4*>(a.qs + size_t(c) * a.K + size_t(blk) * 32);
-    lo = p[0];
-    hi = p[1];
-    d = a.ds[size_t(c) * (a.K / 32) + blk];
+__device__ __forceinline__ ActBlock load_act(const int8_t* qs, const float4* ds, int K, int c, int blk) {
+    const int4* p = reinterpret_cast<const int4*>(qs + size_t(c) * K + size_t(blk) * 32);
+    return ActBlock{p[0], p[1], ds[size_t(c) * (K / 32) + blk]};
 }
 
 __device__ __forceinline__ int dot8(const uint32_t* w, int4 x0, int4 x1) {
@@ -50,54 +42,64 @@ __device__ __forceinline__ int dot8(const uint32_t* w, int4 x0, int4 x1) {
     return dot4(int(w[7]), x1.w, s);
 }
 
-// ---------------------------------------------------------------- per-type units
-// Each unit adds its contribution to acc[c] (only when ok) and, with SUMS, stores its int32 group sums.
+// ------------------------------------------------------------------------------------------------ weight units
+// Each unit type loads its raw dwords (load), and adds its contribution for one activation column (acc),
+// returning the exact int32 group sums through g[].
 
 // q4_0: 18-byte block {fp16 d, qs[16]}; element j < 16 is the low nibble of qs[j], j + 16 the high nibble.
 // Reference q81: sum over both calls of fma(d, fma(float(dot), d8, -4 s8), acc) with dot over the unsigned
 // nibbles (qmv_model.cpp:151-160); one call per block here: fma(d, fma(float(dot), d8, -8 s8), acc).
-template <int B, bool SUMS>
-__device__ __forceinline__ void unit_q4_0(const uint8_t* row, int u, bool ok, const Act& a, float* acc, int32_t* gs,
-                                          size_t gcol) {
-    uint32_t q[4], dbits;
-    load_q4_0_block(row + size_t(u) * 18, q, dbits);
-    const float d = half_bits_to_float(dbits);
-    uint32_t n[8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        n[j] = q[j] & kLo;
-        n[4 + j] = (q[j] >> 4) & kLo;
+struct UnitQ4_0 {
+    static constexpr int kElems = 32, kGroups = 1, kActBlocks = 1;
+    uint32_t w[5], sh;
+    __device__ __forceinline__ void load(const uint8_t* row, int u) {
+        const uintptr_t a = reinterpret_cast<uintptr_t>(row + size_t(u) * 18);
+        const uint32_t* base = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+        const U32x4 v = ld_u32x4(base);  // reads only dwords holding block bytes (see common.h)
+        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+        w[4] = base[4];
+        sh = uint32_t(a & 2);
     }
+    __device__ __forceinline__ float acc(const ActBlock* x, float a, int32_t* g) const {
+        const uint32_t sel = slice_sel(sh);
+        uint32_t n[8];
 #pragma unroll
-    for (int c = 0; c < B; ++c) {
-        int4 x0, x1;
-        float4 dd;
-        load_act(a, c, u, x0, x1, dd);
-        const int dot = dot8(n, x0, x1);
-        const float v = fmaf(d, fmaf(float(dot), dd.x, -8.0f * dd.y), acc[c]);
-        acc[c] = ok ? v : acc[c];
-        if (SUMS && ok) gs[gcol * c + u] = dot;
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t q = perm(w[j + 1], w[j], sel);
+            n[j] = q & kLo;
+            n[4 + j] = (q >> 4) & kLo;
+        }
+        const float d = half_bits_to_float(sh ? (w[0] >> 16) : w[0]);
+        const int dot = dot8(n, x[0].lo, x[0].hi);
+        g[0] = dot;
+        return fmaf(d, fmaf(float(dot), x[0].ds.x, -8.0f * x[0].ds.y), a);
     }
-}
+};
 
 // q8_0: 34-byte block {fp16 d, int8 qs[32]}; reference: fma(d * d8, float(dot), acc) (qmv_model.cpp:161).
-template <int B, bool SUMS>
-__device__ __forceinline__ void unit_q8_0(const uint8_t* row, int u, bool ok, const Act& a, float* acc, int32_t* gs,
-                                          size_t gcol) {
-    uint32_t q[8], dbits;
-    load_q8_0_block(row + size_t(u) * 34, q, dbits);
-    const float d = half_bits_to_float(dbits);
-#pragma unroll
-    for (int c = 0; c < B; ++c) {
-        int4 x0, x1;
-        float4 dd;
-        load_act(a, c, u, x0, x1, dd);
-        const int dot = dot8(q, x0, x1);
-        const float v = fmaf(d * dd.x, float(dot), acc[c]);
-        acc[c] = ok ? v : acc[c];
-        if (SUMS && ok) gs[gcol * c + u] = dot;
+struct UnitQ8_0 {
+    static constexpr int kElems = 32, kGroups = 1, kActBlocks = 1;
+    uint32_t w[9], sh;
+    __device__ __forceinline__ void load(const uint8_t* row, int u) {
+        const uintptr_t a = reinterpret_cast<uintptr_t>(row + size_t(u) * 34);
+        const uint32_t* base = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+        const U32x4 v0 = ld_u32x4(base), v1 = ld_u32x4(base + 4);
+        w[0] = v0.x; w[1] = v0.y; w[2] = v0.z; w[3] = v0.w;
+        w[4] = v1.x; w[5] = v1.y; w[6] = v1.z; w[7] = v1.w;
+        w[8] = base[8];
+        sh = uint32_t(a & 2);
     }
-}
+    __device__ __forceinline__ float acc(const ActBlock* x, float a, int32_t* g) const {
+        const uint32_t sel = slice_sel(sh);
+        uint32_t q[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) q[j] = perm(w[j + 1], w[j], sel);
+        const float d = half_bits_to_float(sh ? (w[0] >> 16) : w[0]);
+        const int dot = dot8(q, x[0].lo, x[0].hi);
+        g[0] = dot;
+        return fmaf(d * x[0].ds.x, float(dot), a);
+    }
+};
 
 // q4_K: 144-byte super-block {fp16 d, fp16 dmin, scales[12], qs[128]}; a unit is the pair of sub-blocks
 // 2g, 2g+1 that share qs[32g..32g+31] (low / high nibbles). Six-bit scale/min codes as get_scale_min_k4
@@ -113,209 +115,230 @@ __device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t
         mn = int((b2 >> 4) | ((b1 >> 6) << 4));
     }
 }
-
-template <int B, bool SUMS>
-__device__ __forceinline__ void unit_q4_K(const uint8_t* row, int u, bool ok, const Act& a, float* acc, int32_t* gs,
-                                          size_t gcol) {
-    const int blk = u >> 2, g = u & 3;
-    const uint32_t* p = reinterpret_cast<const uint32_t*>(row + size_t(blk) * 144);  // 4-byte aligned
-    const U32x4 hdr = ld_u32x4(p);
-    const U32x4 qa = ld_u32x4(p + 4 + 8 * g), qb = ld_u32x4(p + 8 + 8 * g);
-    const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-    const float d = half_bits_to_float(hdr.x), dmin = half_bits_to_float(hdr.x >> 16);
-    int sc0, mn0, sc1, mn1;
-    q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * g, sc0, mn0);
-    q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * g + 1, sc1, mn1);
-    uint32_t lo[8], hi[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        lo[j] = q[j] & kLo;
-        hi[j] = (q[j] >> 4) & kLo;
+struct UnitQ4_K {
+    static constexpr int kElems = 64, kGroups = 2, kActBlocks = 2;
+    uint32_t hdr[4], q[8];
+    int g;
+    __device__ __forceinline__ void load(const uint8_t* row, int u) {
+        g = u & 3;
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(row + size_t(u >> 2) * 144);  // 4-byte aligned
+        const U32x4 h = ld_u32x4(p), qa = ld_u32x4(p + 4 + 8 * g), qb = ld_u32x4(p + 8 + 8 * g);
+        hdr[0] = h.x; hdr[1] = h.y; hdr[2] = h.z; hdr[3] = h.w;
+        q[0] = qa.x; q[1] = qa.y; q[2] = qa.z; q[3] = qa.w;
+        q[4] = qb.x; q[5] = qb.y; q[6] = qb.z; q[7] = qb.w;
     }
-    const int ab = blk * 8 + 2 * g;  // activation block of sub-block 2g
+    __device__ __forceinline__ float acc(const ActBlock* x, float a, int32_t* gs) const {
+        int sc0, mn0, sc1, mn1;
+        q4k_scale_min(hdr[1], hdr[2], hdr[3], 2 * g, sc0, mn0);
+        q4k_scale_min(hdr[1], hdr[2], hdr[3], 2 * g + 1, sc1, mn1);
+        uint32_t lo[8], hi[8];
 #pragma unroll
-    for (int c = 0; c < B; ++c) {
-        int4 x0, x1, y0, y1;
-        float4 dx, dy;
-        load_act(a, c, ab, x0, x1, dx);
-        load_act(a, c, ab + 1, y0, y1, dy);
-        const int d0 = dot8(lo, x0, x1);
-        const int d1 = dot8(hi, y0, y1);
-        const float sd = fmaf(dy.x, float(d1 * sc1), dx.x * float(d0 * sc0));
-        const float sm = fmaf(dy.x, dy.z * float(mn1), dx.x * (dx.z * float(mn0)));
-        const float v = acc[c] + fmaf(d, sd, -dmin * sm);
-        acc[c] = ok ? v : acc[c];
-        if (SUMS && ok) {
-            gs[gcol * c + 2 * u] = d0;
-            gs[gcol * c + 2 * u + 1] = d1;
+        for (int j = 0; j < 8; ++j) {
+            lo[j] = q[j] & kLo;
+            hi[j] = (q[j] >> 4) & kLo;
         }
+        const float d = half_bits_to_float(hdr[0]), dmin = half_bits_to_float(hdr[0] >> 16);
+        const int d0 = dot8(lo, x[0].lo, x[0].hi), d1 = dot8(hi, x[1].lo, x[1].hi);
+        gs[0] = d0;
+        gs[1] = d1;
+        const float sd = fmaf(x[1].ds.x, float(d1 * sc1), x[0].ds.x * float(d0 * sc0));
+        const float sm = fmaf(x[1].ds.x, x[1].ds.z * float(mn1), x[0].ds.x * (x[0].ds.z * float(mn0)));
+        return a + fmaf(d, sd, -dmin * sm);
     }
-}
+};
 
 // q6_K: 210-byte super-block {ql[128], qh[64], int8 scales[16], fp16 d}; a unit is one 32-element sub-block s.
 // Element i of s: low 4 bits from ql[(s/4)*64 + (s%2)*32 + i] (low nibble for s%4 < 2, else high), high 2 bits
 // from qh[(s/4)*32 + i] >> 2*(s%4); q6 = value - 32; scale per 16 = scales[2s + i/16] (ggml dequantize_row_q6_K).
 // Reference arithmetic (vec_dot_q6_K_q8_1): d * sum(d8 * dot16 * sc) with exact int32 dot16 per 16 elements.
-template <int B, bool SUMS>
-__device__ __forceinline__ void unit_q6_K(const uint8_t* row, int u, bool ok, const Act& a, float* acc, int32_t* gs,
-                                          size_t gcol) {
-    const int blk = u >> 3, s = u & 7;
-    const uint8_t* p = row + size_t(blk) * 210;
-    uint32_t ql[8], qh[8];
-    load_field<8>(p + (s >> 2) * 64 + (s & 1) * 32, ql);
-    load_field<8>(p + 128 + (s >> 2) * 32, qh);
-    const uint32_t sw = load_u16(p + 192 + 2 * s);  // scales[2s], scales[2s+1]
-    const int sc0 = int(int8_t(sw & 255)), sc1 = int(int8_t((sw >> 8) & 255));
-    const float d = half_bits_to_float(load_u16(p + 208));
-    const int nsh = (s & 2) ? 4 : 0, hsh = 2 * (s & 3);
-    uint32_t q6[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const uint32_t v = ((ql[j] >> nsh) & kLo) | (((qh[j] >> hsh) & 0x03030303u) << 4);  // 0..63 per byte
-        q6[j] = ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u;                             // v - 32 per byte
+struct UnitQ6_K {
+    static constexpr int kElems = 32, kGroups = 2, kActBlocks = 1;
+    uint32_t ql[8], qh[8], sw, dw;
+    int s;
+    __device__ __forceinline__ void load(const uint8_t* row, int u) {
+        s = u & 7;
+        const uint8_t* p = row + size_t(u >> 3) * 210;
+        load_field<8>(p + (s >> 2) * 64 + (s & 1) * 32, ql);
+        load_field<8>(p + 128 + (s >> 2) * 32, qh);
+        sw = load_u16(p + 192 + 2 * s);  // scales[2s], scales[2s+1]
+        dw = load_u16(p + 208);
     }
+    __device__ __forceinline__ float acc(const ActBlock* x, float a, int32_t* g) const {
+        const int nsh = (s & 2) ? 4 : 0, hsh = 2 * (s & 3);
+        uint32_t q6[8];
 #pragma unroll
-    for (int c = 0; c < B; ++c) {
-        int4 x0, x1;
-        float4 dd;
-        load_act(a, c, u, x0, x1, dd);
-        int g0 = dot4(int(q6[0]), x0.x, 0);
-        g0 = dot4(int(q6[1]), x0.y, g0);
-        g0 = dot4(int(q6[2]), x0.z, g0);
-        g0 = dot4(int(q6[3]), x0.w, g0);
-        int g1 = dot4(int(q6[4]), x1.x, 0);
-        g1 = dot4(int(q6[5]), x1.y, g1);
-        g1 = dot4(int(q6[6]), x1.z, g1);
-        g1 = dot4(int(q6[7]), x1.w, g1);
-        const float v = fmaf(d * dd.x, float(g0 * sc0 + g1 * sc1), acc[c]);
-        acc[c] = ok ? v : acc[c];
-        if (SUMS && ok) {
-            gs[gcol * c + 2 * u] = g0;
-            gs[gcol * c + 2 * u + 1] = g1;
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t v = ((ql[j] >> nsh) & kLo) | (((qh[j] >> hsh) & 0x03030303u) << 4);  // 0..63 per byte
+            q6[j] = ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u;                             // v - 32 per byte
         }
+        int g0 = dot4(int(q6[0]), x[0].lo.x, 0);
+        g0 = dot4(int(q6[1]), x[0].lo.y, g0);
+        g0 = dot4(int(q6[2]), x[0].lo.z, g0);
+        g0 = dot4(int(q6[3]), x[0].lo.w, g0);
+        int g1 = dot4(int(q6[4]), x[0].hi.x, 0);
+        g1 = dot4(int(q6[5]), x[0].hi.y, g1);
+        g1 = dot4(int(q6[6]), x[0].hi.z, g1);
+        g1 = dot4(int(q6[7]), x[0].hi.w, g1);
+        g[0] = g0;
+        g[1] = g1;
+        const int sc0 = int(int8_t(sw & 255)), sc1 = int(int8_t((sw >> 8) & 255));
+        return fmaf(half_bits_to_float(dw) * x[0].ds.x, float(g0 * sc0 + g1 * sc1), a);
     }
-}
-
-template <int TYPE>
-struct Unit {
-    static constexpr int elems = TYPE == Q4_K ? 64 : 32;
-    static constexpr int groups = TYPE == Q4_0 || TYPE == Q8_0 ? 1 : 2;  // int32 sums per unit
 };
 
-template <int TYPE, int B, bool SUMS>
-__device__ __forceinline__ void unit(const uint8_t* row, int u, bool ok, const Act& a, float* acc, int32_t* gs,
-                                     size_t gcol) {
-    if constexpr (TYPE == Q4_0) unit_q4_0<B, SUMS>(row, u, ok, a, acc, gs, gcol);
-    if constexpr (TYPE == Q8_0) unit_q8_0<B, SUMS>(row, u, ok, a, acc, gs, gcol);
-    if constexpr (TYPE == Q4_K) unit_q4_K<B, SUMS>(row, u, ok, a, acc, gs, gcol);
-    if constexpr (TYPE == Q6_K) unit_q6_K<B, SUMS>(row, u, ok, a, acc, gs, gcol);
+template <int TYPE> struct UnitOf;
+template <> struct UnitOf<Q4_0> { using T = UnitQ4_0; };
+template <> struct UnitOf<Q8_0> { using T = UnitQ8_0; };
+template <> struct UnitOf<Q4_K> { using T = UnitQ4_K; };
+template <> struct UnitOf<Q6_K> { using T = UnitQ6_K; };
+
+// Units per lane per pass: register budget for B activation columns (more columns, fewer units).
+template <int TYPE, int B>
+constexpr int units_per_lane() {
+    if (TYPE == Q4_K || TYPE == Q6_K) return 1;
+    return B <= 2 ? 2 : 1;
 }
 
-template <int TYPE, int B, bool SUMS>
-__global__ __launch_bounds__(256) void k_mmvq(const uint8_t* __restrict__ w, int64_t nb01, int M, int K, int tlog2,
+// ------------------------------------------------------------------------------------------------ reduction
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
+}
+// Sum over the wave's 64 lanes; lane 0 holds the total. DPP within each row of 16, then rows combined.
+__device__ __forceinline__ float wave_total(float v) {
+    v += dpp<0xB1>(v);   // quad_perm xor 1
+    v += dpp<0x4E>(v);   // quad_perm xor 2
+    v += dpp<0x141>(v);  // row_half_mirror
+    v += dpp<0x140>(v);  // row_mirror
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+template <int TYPE, int B, int RW, bool SUMS>
+__global__ __launch_bounds__(256) void k_mmvq(const uint8_t* __restrict__ w, int64_t nb01, int M, int K,
                                               const int8_t* __restrict__ xq, const float4* __restrict__ xds,
                                               float* __restrict__ y, int32_t* __restrict__ gs) {
-    const int T = 1 << tlog2;
-    const int t = threadIdx.x & (T - 1);
-    const int m = blockIdx.x * (256 >> tlog2) + (threadIdx.x >> tlog2);
-    const int units = K / Unit<TYPE>::elems;
-    const Act a{xq, xds, K};
-    float acc[B];
+    using U = typename UnitOf<TYPE>::T;
+    constexpr int UB = units_per_lane<TYPE, B>();
+    const int lane = threadIdx.x & 63;
+    const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RW;
+    if (r0 >= M) return;  // the whole wave leaves; nothing below synchronizes across waves
+    const int units = K / U::kElems;
+    const int glen = units * U::kGroups;  // int32 sums per row and column
+    float acc[RW][B];
 #pragma unroll
-    for (int c = 0; c < B; ++c) acc[c] = 0.0f;
-    if (m < M && t < units) {
-        const uint8_t* row = w + size_t(m) * nb01;
-        const int glen = units * Unit<TYPE>::groups;           // int32 sums per row
-        int32_t* grow = SUMS ? gs + size_t(m) * glen : nullptr;  // column c adds c * M * glen
-        const size_t gcol = size_t(M) * glen;
-        constexpr int kBatch = batch<TYPE, B>();
-        for (int u0 = t; u0 < units; u0 += kBatch * T) {
+    for (int r = 0; r < RW; ++r)
 #pragma unroll
-            for (int i = 0; i < kBatch; ++i) {
-                const int u = u0 + i * T;
-                const bool ok = u < units;
-                unit<TYPE, B, SUMS>(row, ok ? u : u0, ok, a, acc, grow, gcol);
+        for (int c = 0; c < B; ++c) acc[r][c] = 0.0f;
+
+    for (int kc = 0; kc < units; kc += 64 * UB) {
+        int uu[UB];
+        bool uok[UB];
+        ActBlock x[UB][B][U::kActBlocks];
+#pragma unroll
+        for (int i = 0; i < UB; ++i) {
+            const int u = kc + lane + 64 * i;
+            uok[i] = u < units;
+            uu[i] = uok[i] ? u : 0;
+#pragma unroll
+            for (int c = 0; c < B; ++c)
+#pragma unroll
+                for (int ab = 0; ab < U::kActBlocks; ++ab)
+                    x[i][c][ab] = load_act(xq, xds, K, c, uu[i] * U::kActBlocks + ab);
+        }
+        U wu[RW][UB];
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+            const int row = min(r0 + r, M - 1);
+            const uint8_t* wr = w + size_t(row) * nb01;
+#pragma unroll
+            for (int i = 0; i < UB; ++i) wu[r][i].load(wr, uu[i]);
+        }
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+            const bool rok = r0 + r < M;
+#pragma unroll
+            for (int i = 0; i < UB; ++i) {
+#pragma unroll
+                for (int c = 0; c < B; ++c) {
+                    int32_t g[U::kGroups];
+                    const float v = wu[r][i].acc(x[i][c], acc[r][c], g);
+                    acc[r][c] = uok[i] ? v : acc[r][c];
+                    if (SUMS && uok[i] && rok) {
+                        int32_t* dst = gs + (size_t(c) * M + r0 + r) * glen + size_t(uu[i]) * U::kGroups;
+#pragma unroll
+                        for (int k = 0; k < U::kGroups; ++k) dst[k] = g[k];
+                    }
+                }
             }
         }
     }
-    // Reduce over the T threads of each row.
-    __shared__ float red[4][B];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
-    for (int c = 0; c < B; ++c) acc[c] = group_sum(acc[c], T < 64 ? T : 64);
-    if (T <= 64) {
-        if (t == 0 && m < M) {
-#pragma unroll
-            for (int c = 0; c < B; ++c) y[size_t(c) * M + m] = acc[c];
-        }
-        return;
-    }
-    if (lane == 0) {
-#pragma unroll
-        for (int c = 0; c < B; ++c) red[wave][c] = acc[c];
-    }
-    __syncthreads();
-    if (t == 0 && m < M) {
-        const int waves = T >> 6;
+    for (int r = 0; r < RW; ++r) {
 #pragma unroll
         for (int c = 0; c < B; ++c) {
-            float s = 0.0f;
-            for (int i = 0; i < waves; ++i) s += red[wave + i][c];
-            y[size_t(c) * M + m] = s;
+            const float t = wave_total(acc[r][c]);
+            if (lane == 0 && r0 + r < M) y[size_t(c) * M + r0 + r] = t;
         }
     }
 }
 
 template <int TYPE, int B>
-hipError_t launch_b(const uint8_t* w, int64_t nb01, int M, int K, int tlog2, const int8_t* xq, const float4* xds,
+hipError_t launch_b(const uint8_t* w, int64_t nb01, int M, int K, int rw, const int8_t* xq, const float4* xds,
                     float* y, int32_t* gs, hipStream_t stream) {
-    const int rows_per_wg = 256 >> tlog2;
-    const dim3 grid((M + rows_per_wg - 1) / rows_per_wg);
-    if (gs)
-        hipLaunchKernelGGL((k_mmvq<TYPE, B, true>), grid, dim3(256), 0, stream, w, nb01, M, K, tlog2, xq, xds, y, gs);
-    else
-        hipLaunchKernelGGL((k_mmvq<TYPE, B, false>), grid, dim3(256), 0, stream, w, nb01, M, K, tlog2, xq, xds, y,
-                           gs);
-    return hipGetLastError();
+    if (gs) rw = 1;  // the group-sum export is a check path: one row per wave
+    const dim3 grid((M + 4 * rw - 1) / (4 * rw));
+#define P1X_RW(R)                                                                                                \
+    if (rw == R) {                                                                                               \
+        if (gs) hipLaunchKernelGGL((k_mmvq<TYPE, B, R, true>), grid, dim3(256), 0, stream, w, nb01, M, K, xq, xds, \
+                                   y, gs);                                                                       \
+        else hipLaunchKernelGGL((k_mmvq<TYPE, B, R, false>), grid, dim3(256), 0, stream, w, nb01, M, K, xq, xds, \
+                                y, gs);                                                                          \
+        return hipGetLastError();                                                                                \
+    }
+    P1X_RW(1)
+    P1X_RW(2)
+    P1X_RW(4)
+#undef P1X_RW
+    return hipErrorInvalidValue;
 }
 
 template <int TYPE>
-hipError_t launch_type(int B, const uint8_t* w, int64_t nb01, int M, int K, int tlog2, const int8_t* xq,
+hipError_t launch_type(int B, const uint8_t* w, int64_t nb01, int M, int K, int rw, const int8_t* xq,
                        const float4* xds, float* y, int32_t* gs, hipStream_t stream) {
     switch (B) {
-        case 1: return launch_b<TYPE, 1>(w, nb01, M, K, tlog2, xq, xds, y, gs, stream);
-        case 2: return launch_b<TYPE, 2>(w, nb01, M, K, tlog2, xq, xds, y, gs, stream);
-        case 3: return launch_b<TYPE, 3>(w, nb01, M, K, tlog2, xq, xds, y, gs, stream);
-        case 4: return launch_b<TYPE, 4>(w, nb01, M, K, tlog2, xq, xds, y, gs, stream);
-        case 5: return launch_b<TYPE, 5>(w, nb01, M, K, tlog2, xq, xds, y, gs, stream);
-        case 6: return launch_b<TYPE, 6>(w, nb01, M, K, tlog2, xq, xds, y, gs, stream);
-        case 7: return launch_b<TYPE, 7>(w, nb01, M, K, tlog2, xq, xds, y, gs, stream);
-        case 8: return launch_b<TYPE, 8>(w, nb01, M, K, tlog2, xq, xds, y, gs, stream);
+        case 1: return launch_b<TYPE, 1>(w, nb01, M, K, rw, xq, xds, y, gs, stream);
+        case 2: return launch_b<TYPE, 2>(w, nb01, M, K, rw, xq, xds, y, gs, stream);
+        case 3: return launch_b<TYPE, 3>(w, nb01, M, K, rw, xq, xds, y, gs, stream);
+        case 4: return launch_b<TYPE, 4>(w, nb01, M, K, rw, xq, xds, y, gs, stream);
+        case 5: return launch_b<TYPE, 5>(w, nb01, M, K, rw, xq, xds, y, gs, stream);
+        case 6: return launch_b<TYPE, 6>(w, nb01, M, K, rw, xq, xds, y, gs, stream);
+        case 7: return launch_b<TYPE, 7>(w, nb01, M, K, rw, xq, xds, y, gs, stream);
+        case 8: return launch_b<TYPE, 8>(w, nb01, M, K, rw, xq, xds, y, gs, stream);
     }
     return hipErrorInvalidValue;
 }
 
 }  // namespace
 
-// Threads per row: enough work-groups to cover the 256 CUs several times, and at least one unit per thread.
-int mmvq_threads_log2(int type, int M, int K) {
-    const int units = K / (type == Q4_K ? 64 : 32);
-    int tl = 6;                                                             // one wave per row
-    while (tl < 8 && (M >> (8 - tl)) < 1024 && units >= (2 << tl)) ++tl;  // few rows: more threads per row
-    while (tl > 5 && units < (1 << tl)) --tl;                               // short rows: fewer threads per row
-    return tl;
+// Rows per wave: the most (up to 4) that still leaves >= 2048 waves (8 per CU) to fill the 256 CUs.
+int mmvq_rows_per_wave(int M) {
+    for (int rw : {4, 2})
+        if (M / rw >= 2048) return rw;
+    return 1;
 }
 
 hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
                        float* y, int32_t* gs, hipStream_t stream) {
-    const int tl = mmvq_threads_log2(type, M, K);
+    const int rw = mmvq_rows_per_wave(M);
     const auto* wb = static_cast<const uint8_t*>(w);
     const auto* d4 = reinterpret_cast<const float4*>(xds);
     switch (type) {
-        case Q4_0: return launch_type<Q4_0>(B, wb, nb01, M, K, tl, xq, d4, y, gs, stream);
-        case Q8_0: return launch_type<Q8_0>(B, wb, nb01, M, K, tl, xq, d4, y, gs, stream);
-        case Q4_K: return launch_type<Q4_K>(B, wb, nb01, M, K, tl, xq, d4, y, gs, stream);
-        case Q6_K: return launch_type<Q6_K>(B, wb, nb01, M, K, tl, xq, d4, y, gs, stream);
+        case Q4_0: return launch_type<Q4_0>(B, wb, nb01, M, K, rw, xq, d4, y, gs, stream);
+        case Q8_0: return launch_type<Q8_0>(B, wb, nb01, M, K, rw, xq, d4, y, gs, stream);
+        case Q4_K: return launch_type<Q4_K>(B, wb, nb01, M, K, rw, xq, d4, y, gs, stream);
+        case Q6_K: return launch_type<Q6_K>(B, wb, nb01, M, K, rw, xq, d4, y, gs, stream);
     }
     return hipErrorInvalidValue;
 }

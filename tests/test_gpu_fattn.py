@@ -1,7 +1,7 @@
 """GPU parity of the split-K FlashAttention decode against the FP64 oracle (p100::attention_reference).
 
 Bar: include/p100/tolerance.h:20-31 element-wise (|o-ref| <= 1e-3 + 2e-3|ref|, LSE within 1e-3, -inf exact),
-and the north star's "max relative error <= 2e-3" read as max|o-ref| / max|ref| (tests/error_budget.cpp:78).
+and the path's stated "max relative error <= 2e-3" read as max|o-ref| / max|ref| (tests/error_budget.cpp:78).
 Inputs are rounded to fp16 (the kernel's K/V type) on the host; Q stays fp32. Shapes: the decode config
 (32 query heads / 8 KV heads, d 128, 1 query row, KV 512..32768, causal), plus GQA ratios 1..8, d 64 / 256,
 batch 2, several query rows with bottom-right causal alignment, masks with fully masked rows, softcap,

@@ -1,6 +1,6 @@
 """GPU parity of the mat-vec path against the CPU oracle on identical seeded inputs.
 
-Bars (the north star's, written here):
+Bars (the decode path's stated accuracy contract, written here):
 * Q8_1 activation (q, d, s and the integer sum) and the h16 pre-pass: bit-exact with the oracle's prepare().
 * int32 group sums of the Q8_1 path: bit-exact.
 * FP32 outputs: |y - oracle| <= 1e-5 * ||w_row|| * ||x|| against the oracle's value of the same path (same
