@@ -116,7 +116,14 @@ def main():
     timer = GraphTimer(torch)
     torch.cuda.synchronize()
     if args.only == "roofline":
-        print(json.dumps({"only": "roofline", "roofline": measure_roofline(torch, P, lib, timer, layers, xs[14336])}))
+        roof = measure_roofline(torch, P, lib, timer, layers, xs[14336])
+        # Calibration for hardware byte counters: a plain 32 MiB device copy (reads and writes 33,554,432 B).
+        src = torch.empty(32 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"only": "roofline", "roofline": roof, "calibration_copy_bytes": 32 << 20}))
         return
     if args.only == "fa":
         print(json.dumps({"only": "fa", "fa_decode": measure_fa(torch, P, lib, timer, gen, args.fa_ctx)}))

@@ -113,7 +113,9 @@ int p1x_attn_validate(const p1x_attn_params* p);
  * (additive, -inf masks out); o f32 [batch][n_head_q][seq_q][d_v]; lse optional f32 [batch][n_head_q][seq_q]
  * (natural log; -inf for a row with no visible key, whose o is 0).
  * Supported: d_qk == d_v in {64, 128, 256}. Each query row is decoded independently, so seq_q > 1 works
- * but re-reads K/V per row (this is the decode path). ws >= p1x_flash_attn_decode_workspace(p) bytes.
+ * but re-reads K/V per row (this is the decode path). ws >= p1x_flash_attn_decode_workspace(p) bytes,
+ * 16-byte aligned, contents arbitrary (it holds the KV-split partials between the two launches; when the
+ * plan has a single split the size is 0 and ws may be null).
  */
 size_t p1x_flash_attn_decode_workspace(const p1x_attn_params* p);
 int p1x_flash_attn_decode(const p1x_attn_params* p, const float* q, const uint16_t* k, const uint16_t* v,

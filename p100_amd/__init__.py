@@ -236,6 +236,7 @@ def validate(p: AttnParams) -> str:
 
 
 def flash_attn_decode_workspace(p: AttnParams) -> int:
+    """Bytes of device workspace for flash_attn_decode (0 when the KV range is not split)."""
     return load().p1x_flash_attn_decode_workspace(C.byref(_params(p)))
 
 

@@ -192,11 +192,12 @@ int p1x_attn_validate(const p1x_attn_params* p) {
     return P1X_OK;
 }
 
+// Workspace: the split partials, O [groups][splits][heads][d] then (max, sum) [groups][splits][heads].
 size_t p1x_flash_attn_decode_workspace(const p1x_attn_params* p) {
     if (!p || attn_reason(p)) return 0;
     int splits = 0, chunk = 0;
-    p1x::fa_split_plan(p->batch, p->n_head_q, p->n_head_kv, p->seq_q, p->seq_kv, splits, chunk);
-    return size_t(p->batch) * p->n_head_q * p->seq_q * splits * (p->d_v + 2) * sizeof(float);
+    p1x::fa_split_plan(p->batch, p->n_head_q, p->n_head_kv, p->seq_q, p->seq_kv, p->d_qk, splits, chunk);
+    return splits == 1 ? 0 : size_t(p->batch) * p->n_head_q * p->seq_q * splits * (p->d_v + 2) * sizeof(float);
 }
 
 int p1x_flash_attn_decode(const p1x_attn_params* p, const float* q, const uint16_t* k, const uint16_t* v,
@@ -207,8 +208,9 @@ int p1x_flash_attn_decode(const p1x_attn_params* p, const float* q, const uint16
     if (!q || !k || !v || !o) return fail(P1X_EINVAL, "null q, k, v or o pointer");
     if (p->d_qk != p->d_v || (p->d_qk != 64 && p->d_qk != 128 && p->d_qk != 256))
         return fail(P1X_EUNSUPPORTED, "decode kernel supports d_qk == d_v in {64, 128, 256}");
-    if (p->seq_q > 65535 || int64_t(p->batch) * p->n_head_kv > 65535)
-        return fail(P1X_EUNSUPPORTED, "seq_q and batch*n_head_kv must be <= 65535");
+    const int64_t head_chunks = (p->n_head_q / p->n_head_kv) / p1x::fa_heads_per_wg(p->n_head_q, p->n_head_kv);
+    if (p->seq_q > 65535 || int64_t(p->batch) * p->n_head_kv * head_chunks > 65535)
+        return fail(P1X_EUNSUPPORTED, "seq_q and batch*n_head_kv*(query heads per KV head / heads per group) must be <= 65535");
     if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16))
         return fail(P1X_EINVAL, "q, k and v must be 16-byte aligned");
     const int64_t d = p->d_qk;
@@ -217,7 +219,6 @@ int p1x_flash_attn_decode(const p1x_attn_params* p, const float* q, const uint16
     a.k = reinterpret_cast<const __half*>(k);
     a.v = reinterpret_cast<const __half*>(v);
     a.mask = mask;
-    a.part = static_cast<float*>(ws);
     if (strides) {
         a.k_row = strides->k_row, a.k_head = strides->k_head, a.k_batch = strides->k_batch;
         a.v_row = strides->v_row, a.v_head = strides->v_head, a.v_batch = strides->v_batch;
@@ -236,12 +237,17 @@ int p1x_flash_attn_decode(const p1x_attn_params* p, const float* q, const uint16
     a.causal = p->causal != 0;
     a.scale = p->scale == 0.0f ? 1.0f / std::sqrt(float(p->d_qk)) : p->scale;
     a.softcap = p->softcap;
-    p1x::fa_split_plan(p->batch, p->n_head_q, p->n_head_kv, p->seq_q, p->seq_kv, a.splits, a.chunk);
+    p1x::fa_split_plan(p->batch, p->n_head_q, p->n_head_kv, p->seq_q, p->seq_kv, p->d_qk, a.splits, a.chunk);
     const size_t need = p1x_flash_attn_decode_workspace(p);
-    if (!ws || ws_bytes < need)
+    if (need && (!ws || ws_bytes < need))
         return fail(P1X_EWORKSPACE, "workspace of " + std::to_string(need) + " bytes required");
-    if (!aligned(ws, 16)) return fail(P1X_EINVAL, "workspace must be 16-byte aligned");
-    hipError_t e = p1x::launch_fa_decode(a, p->batch, p->d_qk, o, lse, static_cast<hipStream_t>(stream));
+    if (need && !aligned(ws, 16)) return fail(P1X_EINVAL, "workspace must be 16-byte aligned");
+    const size_t n_part = size_t(p->batch) * p->n_head_q * p->seq_q * a.splits;
+    a.part_o = static_cast<float*>(ws);
+    a.part_ml = reinterpret_cast<float2*>(a.part_o + n_part * d);
+    a.o = o;
+    a.lse = lse;
+    hipError_t e = p1x::launch_fa_decode(a, p->batch, p->d_qk, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? P1X_OK : hip_fail(e, "flash_attn_decode");
 }
 

@@ -5,25 +5,45 @@
 // Every accumulation is FP32: logits, running max and sum, and the P*V accumulator (the reference's
 // per-tile FP16 VKQ flush, patch 0004, exists only because its TILE kernel accumulates in FP16).
 //
-// Pass 1 (k_fa_split): one 256-thread work-group per (split of the KV range, KV head, group of NH query heads
-// sharing it, query row). D/8 lanes own one key row (8 fp16 per lane, one 16-byte load), so a wave loads
-// 64*16 consecutive bytes of K or V per instruction; the 256/(D/8) key groups of the work-group interleave
-// over the split's keys, kKeys keys per group per step (all their K and V loads issued together), and each
-// group keeps its own online-softmax state (FP32 m, l, and an 8-wide slice of O for each of the NH heads).
-// Logits are kept in base 2 (scaled by log2 e) so exponentials are v_exp_f32. Groups merge through LDS; the
-// work-group writes one unnormalised partial (O[D], max, sum) per head.
-// Pass 2 (k_fa_combine): per query row, rebase the partials to their common max and divide once
-// (the combine of fattn-common.cuh:963-977 as modelled in attention_tiled_model.cpp:183-222).
+// Pass 1 (k_fa_split): one 256-thread work-group per (split of the KV range, KV head, chunk of NH query heads
+// sharing it, query row). A key row is owned by LPK = D/16 lanes, 16 dimensions each (the two 8-element halves
+// [8l, 8l+8) and [D/2 + 8l, D/2 + 8l + 8), so one load instruction reads whole 128-byte lines of GPW = 64/LPK
+// consecutive rows). Each group of LPK lanes takes kKeys keys per batch; a batch's K and V loads are issued one
+// batch ahead of its arithmetic (two register buffers), with non-temporal hints since no element is read twice.
+// Softmax: each wave keeps one reference max per head, shared by its groups, and raises it (rescaling the sums,
+// a wave-uniform branch) only when a logit exceeds it by more than kTau, so after the first batch it rarely
+// moves; probabilities are 2^(x - ref) <= 2^kTau, and the groups' partial sums merge by plain addition (DPP
+// row rotation inside each 16-lane row, then LDS across rows and waves); the work-group writes one
+// unnormalised partial (O, max, sum) per head.
+// Pass 2 (k_fa_combine): one wave per output row rebases every split's partial to the common max and sums
+// (one round of loads per 32 splits). With a single split, pass 1 writes O and LSE itself and pass 2 is skipped.
+// (A single-launch variant, where the last work-group to arrive combines after an agent-scope release/acquire
+// pair, measured 2.4x slower at ctx 8192: each agent-scope release writes back the XCD's L2.)
 #include "common.h"
 #include "launch.h"
+
+#ifndef P1X_FA_PF
+#define P1X_FA_PF 2  // K/V batches in flight per wave
+#endif
+#ifndef P1X_FA_TARGET_WGS
+#define P1X_FA_TARGET_WGS 256  // pass-1 work-groups aimed for: one per CU, a wave per SIMD
+#endif
 
 namespace p1x {
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
-constexpr int kKeys = 4;         // keys per group per step
+constexpr int kKeys = 2;         // keys per group per batch
+constexpr int kWaves = 4;        // waves per pass-1 work-group
 constexpr int kMaxSplits = 256;  // fa_split_plan never exceeds this
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 ld_stream(const __half* p) {  // 16-byte load, non-temporal (read once)
+    const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(t.x, t.y, t.z, t.w);
+}
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
@@ -32,16 +52,33 @@ __device__ __forceinline__ float dpp_f(float v) {
 // DPP controls: quad_perm(1,0,3,2) = xor 1, quad_perm(2,3,0,1) = xor 2, row_half_mirror, row_mirror.
 constexpr int kXor1 = 0xB1, kXor2 = 0x4E, kHalfMirror = 0x141, kMirror = 0x140;
 
-// Sum over the aligned group of W (8, 16 or 32) lanes that own one key row; every lane gets the total.
+// Sum over the aligned group of W (4, 8 or 16) lanes that own one key row; every lane gets the total.
 template <int W>
 __device__ __forceinline__ float key_sum(float v) {
     v += dpp_f<kXor1>(v);
     v += dpp_f<kXor2>(v);
-    v += dpp_f<kHalfMirror>(v);
+    if constexpr (W >= 8) v += dpp_f<kHalfMirror>(v);
     if constexpr (W >= 16) v += dpp_f<kMirror>(v);
-    if constexpr (W >= 32)  // xor 16 inside each 32-lane half: ds_swizzle bit mode, and 0x1f, xor 0x10
-        v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
     return v;
+}
+
+constexpr int kRor4 = 0x124, kRor8 = 0x128;  // DPP row_ror:4 and row_ror:8 (lane ^ 8 inside a 16-lane row)
+
+// Sum over the groups of one 16-lane row that share l = lane % LPK; every lane of the row gets its row's sum.
+template <int LPK>
+__device__ __forceinline__ float row_group_sum(float v) {
+    if constexpr (LPK <= 8) v += dpp_f<kRor8>(v);
+    if constexpr (LPK <= 4) v += dpp_f<kRor4>(v);  // after ror 8 lanes i and i ^ 8 agree, so ror 4 completes it
+    return v;
+}
+// Max over all groups of the wave (every lane gets it): DPP inside rows, ds_swizzle across the two rows of each
+// 32-lane half, ds_bpermute across halves.
+template <int LPK>
+__device__ __forceinline__ float wave_group_max(float v) {
+    if constexpr (LPK <= 8) v = fmaxf(v, dpp_f<kRor8>(v));
+    if constexpr (LPK <= 4) v = fmaxf(v, dpp_f<kRor4>(v));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F)));
+    return fmaxf(v, __shfl_xor(v, 32));
 }
 
 __device__ __forceinline__ void h8_to_f32(uint4 v, float* out) {
@@ -54,253 +91,377 @@ __device__ __forceinline__ void h8_to_f32(uint4 v, float* out) {
     }
 }
 
+// Logits may exceed the wave's reference max by up to 2^kTau before the reference is raised (p <= 2^8).
+constexpr float kTau = 8.0f;
+
 template <int D, int NH>
 __global__ __launch_bounds__(256) void k_fa_split(FaArgs a) {
-    constexpr int LPK = D / 8;      // lanes per key row
-    constexpr int G = 256 / LPK;    // key groups per work-group
-    const int g = threadIdx.x / LPK, l = threadIdx.x % LPK;
+    constexpr int LPK = D / 16;     // lanes per key row
+    constexpr int GPW = 64 / LPK;   // key groups per wave
+    constexpr int KPB = kWaves * GPW * kKeys;  // keys per work-group batch
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane / LPK, l = lane % LPK;
     const int split = blockIdx.x;
     const int kvh_all = blockIdx.y / a.head_chunks, hc = blockIdx.y % a.head_chunks;
     const int b = kvh_all / a.hkv, kvh = kvh_all % a.hkv;
     const int i = blockIdx.z;
-    const int group = a.hq / a.hkv;
-    const int h0 = kvh * group + hc * NH;
+    const int h0 = kvh * (a.hq / a.hkv) + hc * NH;
 
-    // Visible keys [0, j_end); this split's share [j0, j1).
+    // Visible keys [0, j_end); this work-group's share [j0, j1).
     const int j_end = a.causal ? min(a.seq_kv, i + (a.seq_kv - a.seq_q) + 1) : a.seq_kv;
     const int j0 = split * a.chunk;
     const int j1 = min(j0 + a.chunk, j_end);
 
     const bool cap = a.softcap > 0.0f;
     const float qmul = cap ? a.scale : a.scale * kLog2e;
-    float qr[NH][8];
+    float qr[NH][16];
 #pragma unroll
     for (int hh = 0; hh < NH; ++hh) {
         const float* qp = a.q + ((size_t(b) * a.hq + h0 + hh) * a.seq_q + i) * D + 8 * l;
-        const float4 x0 = *reinterpret_cast<const float4*>(qp), x1 = *reinterpret_cast<const float4*>(qp + 4);
-        qr[hh][0] = x0.x * qmul; qr[hh][1] = x0.y * qmul; qr[hh][2] = x0.z * qmul; qr[hh][3] = x0.w * qmul;
-        qr[hh][4] = x1.x * qmul; qr[hh][5] = x1.y * qmul; qr[hh][6] = x1.z * qmul; qr[hh][7] = x1.w * qmul;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const float4 x0 = *reinterpret_cast<const float4*>(qp + half * (D / 2));
+            const float4 x1 = *reinterpret_cast<const float4*>(qp + half * (D / 2) + 4);
+            float* r = qr[hh] + 8 * half;
+            r[0] = x0.x * qmul; r[1] = x0.y * qmul; r[2] = x0.z * qmul; r[3] = x0.w * qmul;
+            r[4] = x1.x * qmul; r[5] = x1.y * qmul; r[6] = x1.z * qmul; r[7] = x1.w * qmul;
+        }
     }
-    float m[NH], s[NH], o[NH][8];
+    // Softmax state: a wave-uniform reference max per head, and per-lane partial sums (group-local keys).
+    float mref[NH], s[NH], o[NH][16];
 #pragma unroll
     for (int hh = 0; hh < NH; ++hh) {
-        m[hh] = -INFINITY;
+        mref[hh] = -INFINITY;
         s[hh] = 0.0f;
 #pragma unroll
-        for (int d = 0; d < 8; ++d) o[hh][d] = 0.0f;
+        for (int d = 0; d < 16; ++d) o[hh][d] = 0.0f;
     }
     const __half* kb = a.k + size_t(b) * a.k_batch + size_t(kvh) * a.k_head + 8 * l;
     const __half* vb = a.v + size_t(b) * a.v_batch + size_t(kvh) * a.v_head + 8 * l;
     const float* mrow = a.mask ? a.mask + size_t(i) * a.seq_kv : nullptr;
 
-    for (int jb = j0 + g; jb < j1; jb += G * kKeys) {
-        // Branch-free batch: keys past j1 reload key jb (valid) and get logit -inf.
-        uint4 kr[kKeys], vr[kKeys];
-        bool ok[kKeys];
+    // Key of (batch t, slot u) for this lane's group: the GPW groups of a wave read GPW consecutive rows.
+    const int nb = j1 > j0 ? (j1 - j0 + KPB - 1) / KPB : 0;
+    auto key_of = [&](int t, int u) { return j0 + t * KPB + (wave * kKeys + u) * GPW + g; };
+    struct Buf {
+        uint4 k[kKeys][2], v[kKeys][2];
+    };
+    auto load = [&](Buf& bf, int t) {
 #pragma unroll
         for (int u = 0; u < kKeys; ++u) {
-            const int j = jb + u * G;
-            ok[u] = j < j1;
-            const int jc = ok[u] ? j : jb;
-            kr[u] = *reinterpret_cast<const uint4*>(kb + size_t(jc) * a.k_row);
-            vr[u] = *reinterpret_cast<const uint4*>(vb + size_t(jc) * a.v_row);
+            const int j = key_of(t, u);
+            const int jc = j < j1 ? j : j0;  // keys past the share reload a valid row; their logit becomes -inf
+            const __half* kr = kb + size_t(jc) * a.k_row;
+            const __half* vr = vb + size_t(jc) * a.v_row;
+            bf.k[u][0] = ld_stream(kr);
+            bf.k[u][1] = ld_stream(kr + D / 2);
+            bf.v[u][0] = ld_stream(vr);
+            bf.v[u][1] = ld_stream(vr + D / 2);
         }
+    };
+    auto compute = [&](const Buf& bf, int t) {
         float x[kKeys][NH];
 #pragma unroll
         for (int u = 0; u < kKeys; ++u) {
-            float kf[8];
-            h8_to_f32(kr[u], kf);
+            float kf[16];
+            h8_to_f32(bf.k[u][0], kf);
+            h8_to_f32(bf.k[u][1], kf + 8);
 #pragma unroll
             for (int hh = 0; hh < NH; ++hh) {
-                float dot = 0.0f;
+                float d0 = 0.0f, d1 = 0.0f;
 #pragma unroll
-                for (int d = 0; d < 8; ++d) dot = fmaf(qr[hh][d], kf[d], dot);
-                x[u][hh] = key_sum<LPK>(dot);
+                for (int d = 0; d < 8; ++d) {
+                    d0 = fmaf(qr[hh][d], kf[d], d0);
+                    d1 = fmaf(qr[hh][8 + d], kf[8 + d], d1);
+                }
+                x[u][hh] = key_sum<LPK>(d0 + d1);
             }
+            const int j = key_of(t, u);
+            const bool ok = j < j1;
             if (cap || mrow) {
-                const float add = (mrow && ok[u]) ? mrow[jb + u * G] : 0.0f;
+                const float add = (mrow && ok) ? mrow[j] : 0.0f;
 #pragma unroll
                 for (int hh = 0; hh < NH; ++hh)
                     x[u][hh] = cap ? (a.softcap * tanhf(x[u][hh] / a.softcap) + add) * kLog2e : x[u][hh] + add * kLog2e;
             }
 #pragma unroll
-            for (int hh = 0; hh < NH; ++hh) x[u][hh] = ok[u] ? x[u][hh] : -INFINITY;
+            for (int hh = 0; hh < NH; ++hh) x[u][hh] = ok ? x[u][hh] : -INFINITY;
         }
-        float vf[kKeys][8];
+        bool need = false;
 #pragma unroll
-        for (int u = 0; u < kKeys; ++u) h8_to_f32(vr[u], vf[u]);
+        for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+            for (int u = 0; u < kKeys; ++u) need |= x[u][hh] > mref[hh] + kTau;
+        if (__any(need)) {  // wave-uniform: raise the reference to the wave's max, rescaling what was summed
+#pragma unroll
+            for (int hh = 0; hh < NH; ++hh) {
+                float bm = x[0][hh];
+#pragma unroll
+                for (int u = 1; u < kKeys; ++u) bm = fmaxf(bm, x[u][hh]);
+                bm = wave_group_max<LPK>(bm);  // the same value in every lane
+                const float mn = fmaxf(mref[hh], bm);
+                if (mn > mref[hh]) {
+                    const float alpha = mref[hh] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mref[hh] - mn);
+                    s[hh] *= alpha;
+#pragma unroll
+                    for (int d = 0; d < 16; ++d) o[hh][d] *= alpha;
+                    mref[hh] = mn;
+                }
+            }
+        }
+        float vf[kKeys][16];
+#pragma unroll
+        for (int u = 0; u < kKeys; ++u) {
+            h8_to_f32(bf.v[u][0], vf[u]);
+            h8_to_f32(bf.v[u][1], vf[u] + 8);
+        }
 #pragma unroll
         for (int hh = 0; hh < NH; ++hh) {
-            float tmax = x[0][hh];
-#pragma unroll
-            for (int u = 1; u < kKeys; ++u) tmax = fmaxf(tmax, x[u][hh]);
-            const float mn = fmaxf(m[hh], tmax);
-            if (mn == -INFINITY) continue;  // nothing visible yet for this state
-            const float alpha = exp2f(m[hh] - mn);
-            float p[kKeys], psum = 0.0f;
+            const float base = mref[hh] == -INFINITY ? 0.0f : mref[hh];  // all keys so far masked: p = 0
+            float p[kKeys];
 #pragma unroll
             for (int u = 0; u < kKeys; ++u) {
-                p[u] = exp2f(x[u][hh] - mn);
-                psum += p[u];
+                p[u] = __builtin_amdgcn_exp2f(x[u][hh] - base);
+                s[hh] += p[u];
             }
-            s[hh] = fmaf(s[hh], alpha, psum);
 #pragma unroll
-            for (int d = 0; d < 8; ++d) {
-                float t = o[hh][d] * alpha;
+            for (int d = 0; d < 16; ++d) {
+                float acc = o[hh][d];
 #pragma unroll
-                for (int u = 0; u < kKeys; ++u) t = fmaf(p[u], vf[u][d], t);
-                o[hh][d] = t;
+                for (int u = 0; u < kKeys; ++u) acc = fmaf(p[u], vf[u][d], acc);
+                o[hh][d] = acc;
             }
-            m[hh] = mn;
+        }
+    };
+
+    // A ring of PF register buffers: batch t + PF is requested as soon as batch t has been consumed.
+    constexpr int PF = P1X_FA_PF;
+    Buf ring[PF];
+#pragma unroll
+    for (int p = 0; p < PF; ++p)
+        if (p < nb) load(ring[p], p);
+    for (int t0 = 0; t0 < nb; t0 += PF) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {
+            const int t = t0 + p;
+            if (t >= nb) break;
+            compute(ring[p], t);
+            if (t + PF < nb) load(ring[p], t + PF);
         }
     }
 
-    // Merge the G groups through LDS: per head, weights 2^(m_g - M) once, then O columns.
-    __shared__ float sm[G][NH], ss[G][NH], wt[G][NH], hmax[NH], hden[NH];
-    __shared__ float so[G][NH][D];
+    // The groups of a wave share its reference max, so their partial sums merge by plain addition: inside each
+    // 16-lane row with DPP, then the 4 rows of each of the 4 waves through LDS.
 #pragma unroll
     for (int hh = 0; hh < NH; ++hh) {
-        if (l == 0) {
-            sm[g][hh] = m[hh];
-            ss[g][hh] = s[hh];
-        }
+        s[hh] = row_group_sum<LPK>(s[hh]);
 #pragma unroll
-        for (int d = 0; d < 8; ++d) so[g][hh][8 * l + d] = o[hh][d];
+        for (int d = 0; d < 16; ++d) o[hh][d] = row_group_sum<LPK>(o[hh][d]);
     }
-    __syncthreads();
-    if (threadIdx.x < NH) {
-        const int hh = threadIdx.x;
-        float mx = -INFINITY;
-        for (int gg = 0; gg < G; ++gg) mx = fmaxf(mx, sm[gg][hh]);
-        float den = 0.0f;
-        for (int gg = 0; gg < G; ++gg) {
-            const float w = (ss[gg][hh] == 0.0f || mx == -INFINITY) ? 0.0f : exp2f(sm[gg][hh] - mx);
-            wt[gg][hh] = w;
-            den = fmaf(w, ss[gg][hh], den);
+    constexpr int kStates = kWaves * 4;  // one per 16-lane row
+    __shared__ float wm[kWaves][NH], wsum[kStates][NH];
+    __shared__ float wo[kStates][NH][D];
+    const int row16 = lane >> 4, st = wave * 4 + row16;
+    if ((lane & 15) < LPK) {  // the first group of each row holds the row's sums; l = lane & 15 there
+#pragma unroll
+        for (int hh = 0; hh < NH; ++hh) {
+            if (lane == 0) wm[wave][hh] = mref[hh];
+            if (l == 0) wsum[st][hh] = s[hh];
+#pragma unroll
+            for (int d = 0; d < 8; ++d) {
+                wo[st][hh][8 * l + d] = o[hh][d];
+                wo[st][hh][D / 2 + 8 * l + d] = o[hh][8 + d];
+            }
         }
-        hmax[hh] = mx;
-        hden[hh] = den;
     }
     __syncthreads();
+
+    // Work-group partial per head: rebase the 4 waves to their common max. With one split it is the answer.
+    const int grp = blockIdx.y * a.seq_q + i;  // (batch, KV head, head chunk, query row)
+    const size_t row0 = (size_t(b) * a.hq + h0) * a.seq_q + i;  // output row of head hh: row0 + hh * seq_q
     for (int idx = threadIdx.x; idx < NH * D; idx += 256) {
         const int hh = idx / D, d = idx % D;
-        float num = 0.0f;
-#pragma unroll 8
-        for (int gg = 0; gg < G; ++gg) num = fmaf(wt[gg][hh], so[gg][hh][d], num);
-        const size_t row = (size_t(b) * a.hq + h0 + hh) * a.seq_q + i;
-        float* pp = a.part + (row * a.splits + split) * (D + 2);
-        pp[d] = num;
-        if (d == 0) {
-            pp[D] = hmax[hh];
-            pp[D + 1] = hden[hh];
+        float mx = wm[0][hh];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, wm[w][hh]);
+        float num = 0.0f, den = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float wt = wm[w][hh] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(wm[w][hh] - mx);
+            float n = 0.0f, sm = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                n += wo[w * 4 + r][hh][d];
+                sm += wsum[w * 4 + r][hh];
+            }
+            num = fmaf(wt, n, num);
+            den = fmaf(wt, sm, den);
+        }
+        if (a.splits == 1) {
+            const size_t row = row0 + size_t(hh) * a.seq_q;
+            a.o[row * D + d] = den == 0.0f ? 0.0f : num / den;
+            if (a.lse && d == 0) a.lse[row] = den == 0.0f ? -INFINITY : (mx + log2f(den)) * kLn2;
+        } else {
+            const size_t pr = (size_t(grp) * a.splits + split) * NH + hh;
+            a.part_o[pr * D + d] = num;
+            if (d == 0) a.part_ml[pr] = make_float2(mx, den);
         }
     }
+    if (a.splits == 1) return;
+
 }
 
-// One 256-thread work-group per query row. Thread (d = tid % D, part = tid / D) sums splits part, part + P, ...
-template <int D>
-__global__ __launch_bounds__(256) void k_fa_combine(const float* __restrict__ part, int splits, float* __restrict__ o,
-                                                    float* __restrict__ lse) {
-    constexpr int P = 256 / D;
-    __shared__ float w[kMaxSplits];
-    __shared__ float red[256];
-    __shared__ float stat[2];
-    const size_t row = blockIdx.x;
-    const int tid = threadIdx.x;
-    const float* p = part + row * splits * (D + 2);
-    float mx = -INFINITY;
-    for (int sp = tid; sp < splits; sp += 256) mx = fmaxf(mx, p[sp * (D + 2) + D]);
-    red[tid] = mx;
-    __syncthreads();
-    for (int off = 128; off > 0; off >>= 1) {
-        if (tid < off) red[tid] = fmaxf(red[tid], red[tid + off]);
-        __syncthreads();
+// Wave max / sum over all 64 lanes (every lane gets the result): DPP inside rows, then swizzle and bpermute.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<kXor1>(v));
+    v = fmaxf(v, dpp_f<kXor2>(v));
+    v = fmaxf(v, dpp_f<kHalfMirror>(v));
+    v = fmaxf(v, dpp_f<kMirror>(v));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F)));
+    return fmaxf(v, __shfl_xor(v, 32));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_f<kXor1>(v);
+    v += dpp_f<kXor2>(v);
+    v += dpp_f<kHalfMirror>(v);
+    v += dpp_f<kMirror>(v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+    return v + __shfl_xor(v, 32);
+}
+
+// Pass 2: one wave per output row (four rows per work-group). Lane l owns columns [CPL l, CPL l + CPL) of every
+// split's partial, so the weighted sum over splits needs no cross-lane reduction; the split maxima and sums
+// are reduced across lanes once. All loads of a round (kRound splits) are issued before any arithmetic.
+// The combine of fattn-common.cuh:963-977 as modelled in attention_tiled_model.cpp:183-222: rebase each split
+// to the common max, sum, divide once.
+template <int D, int NH>
+__global__ __launch_bounds__(256) void k_fa_combine(FaArgs a, int rows) {
+    constexpr int CPL = D / 64;  // columns per lane
+    constexpr int kRound = 32;   // splits per round of loads
+    __shared__ float wsh[kWaves][kMaxSplits];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row = blockIdx.x * kWaves + wave;
+    if (row >= rows) return;  // whole wave; nothing below synchronizes across waves
+    // Output row (b, h, i) -> group of the split pass and head slot hh inside it.
+    const int i = row % a.seq_q, bh = row / a.seq_q, h = bh % a.hq, b = bh / a.hq;
+    const int group = a.hq / a.hkv, kvh = h / group, rem = h % group, hc = rem / NH, hh = rem % NH;
+    const int grp = ((b * a.hkv + kvh) * a.head_chunks + hc) * a.seq_q + i;
+    const size_t base = size_t(grp) * a.splits * NH + hh;  // partial of split s: base + s * NH
+
+    const float* po = a.part_o + base * D + CPL * lane;
+    float buf[kRound][CPL];
+    auto load_round = [&](int s0) {
+#pragma unroll
+        for (int u = 0; u < kRound; ++u) {
+            const int sp = s0 + u < a.splits ? s0 + u : s0;  // past the end: reload a valid row, weight 0
+            const float* src = po + size_t(sp) * NH * D;
+            if constexpr (CPL == 4) {
+                const float4 t = *reinterpret_cast<const float4*>(src);
+                buf[u][0] = t.x; buf[u][1] = t.y; buf[u][2] = t.z; buf[u][3] = t.w;
+            } else if constexpr (CPL == 2) {
+                const float2 t = *reinterpret_cast<const float2*>(src);
+                buf[u][0] = t.x; buf[u][1] = t.y;
+            } else {
+                buf[u][0] = src[0];
+            }
+        }
+    };
+    load_round(0);  // the first round of partial rows is in flight together with the split statistics
+    float2 ml[kMaxSplits / 64];
+#pragma unroll
+    for (int k = 0; k < kMaxSplits / 64; ++k) {
+        const int sp = lane + 64 * k;
+        ml[k] = sp < a.splits ? a.part_ml[base + size_t(sp) * NH] : make_float2(-INFINITY, 0.0f);
     }
-    mx = red[0];
-    __syncthreads();
+    float mx = ml[0].x;
+#pragma unroll
+    for (int k = 1; k < kMaxSplits / 64; ++k) mx = fmaxf(mx, ml[k].x);
+    mx = wave_max(mx);
     float den = 0.0f;
-    for (int sp = tid; sp < splits; sp += 256) {
-        const float l = p[sp * (D + 2) + D + 1];
-        const float wv = (l == 0.0f || mx == -INFINITY) ? 0.0f : exp2f(p[sp * (D + 2) + D] - mx);
-        w[sp] = wv;
-        den = fmaf(wv, l, den);
+#pragma unroll
+    for (int k = 0; k < kMaxSplits / 64; ++k) {
+        const int sp = lane + 64 * k;
+        const float wv = (ml[k].y == 0.0f || mx == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ml[k].x - mx);
+        if (sp < a.splits) wsh[wave][sp] = wv;
+        den = fmaf(wv, ml[k].y, den);
     }
-    red[tid] = den;
-    __syncthreads();
-    for (int off = 128; off > 0; off >>= 1) {
-        if (tid < off) red[tid] += red[tid + off];
-        __syncthreads();
+    den = wave_sum(den);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // this wave's LDS weights before any lane reads them
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    float acc[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) acc[c] = 0.0f;
+    for (int s0 = 0; s0 < a.splits; s0 += kRound) {
+        if (s0 > 0) load_round(s0);
+#pragma unroll
+        for (int u = 0; u < kRound; ++u) {
+            const float ww = s0 + u < a.splits ? wsh[wave][s0 + u] : 0.0f;
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) acc[c] = fmaf(ww, buf[u][c], acc[c]);
+        }
     }
-    if (tid == 0) stat[0] = red[0];
-    __syncthreads();
-    den = stat[0];
-    const int d = tid % D, pt = tid / D;
-    float num = 0.0f;
-#pragma unroll 4
-    for (int sp = pt; sp < splits; sp += P) num = fmaf(w[sp], p[sp * (D + 2) + d], num);
-    __syncthreads();
-    red[tid] = num;
-    __syncthreads();
-    if (pt == 0) {
-        for (int q = 1; q < P; ++q) num += red[q * D + d];
-        o[row * D + d] = den == 0.0f ? 0.0f : num / den;
-        if (lse && d == 0) lse[row] = den == 0.0f ? -INFINITY : (mx + log2f(den)) * kLn2;
-    }
+    const float inv = den == 0.0f ? 0.0f : 1.0f / den;
+    float* dst = a.o + size_t(row) * D + CPL * lane;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) dst[c] = den == 0.0f ? 0.0f : acc[c] * inv;
+    if (a.lse && lane == 0) a.lse[row] = den == 0.0f ? -INFINITY : (mx + log2f(den)) * kLn2;
 }
 
 template <int D, int NH>
-void launch_split(const FaArgs& a, int batch, hipStream_t stream) {
+hipError_t launch_split(const FaArgs& a, int batch, hipStream_t stream) {
     const dim3 grid(a.splits, batch * a.hkv * a.head_chunks, a.seq_q);
     hipLaunchKernelGGL((k_fa_split<D, NH>), grid, dim3(256), 0, stream, a);
+    if (a.splits == 1) return hipGetLastError();  // the split pass wrote O and LSE
+    const int rows = batch * a.hq * a.seq_q;
+    hipLaunchKernelGGL((k_fa_combine<D, NH>), dim3((rows + kWaves - 1) / kWaves), dim3(256), 0, stream, a, rows);
+    return hipGetLastError();
 }
 
 template <int D>
-hipError_t launch_d(FaArgs a, int batch, int nh, float* o, float* lse, hipStream_t stream) {
+hipError_t launch_d(const FaArgs& a, int batch, int nh, hipStream_t stream) {
     switch (nh) {
-        case 1: launch_split<D, 1>(a, batch, stream); break;
-        case 2: launch_split<D, 2>(a, batch, stream); break;
-        case 4: launch_split<D, 4>(a, batch, stream); break;
-        case 8: launch_split<D, 8>(a, batch, stream); break;
-        default: return hipErrorInvalidValue;
+        case 1: return launch_split<D, 1>(a, batch, stream);
+        case 2: return launch_split<D, 2>(a, batch, stream);
+        case 4: return launch_split<D, 4>(a, batch, stream);
     }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    const dim3 grid(unsigned(size_t(batch) * a.hq * a.seq_q));
-    hipLaunchKernelGGL((k_fa_combine<D>), grid, dim3(256), 0, stream, a.part, a.splits, o, lse);
-    return hipGetLastError();
+    return hipErrorInvalidValue;
 }
 
 }  // namespace
 
-// Heads per work-group: the largest of 8, 4, 2, 1 dividing the GQA group size.
+// Heads per work-group: the largest of 4, 2, 1 dividing the GQA group size.
 int fa_heads_per_wg(int hq, int hkv) {
     const int group = hq / hkv;
-    for (int nh : {8, 4, 2, 1})
+    for (int nh : {4, 2, 1})
         if (group % nh == 0) return nh;
     return 1;
 }
 
-// KV split: aim for ~1024 work-groups in pass 1, at least 64 keys per split, at most kMaxSplits splits.
-void fa_split_plan(int batch, int hq, int hkv, int seq_q, int seq_kv, int& splits, int& chunk) {
+// KV split: chunks of whole work-group batches (4 waves x 64/(d/16) groups x 2 keys), about
+// P1X_FA_TARGET_WGS pass-1 work-groups in total, at most kMaxSplits splits.
+void fa_split_plan(int batch, int hq, int hkv, int seq_q, int seq_kv, int d, int& splits, int& chunk) {
+    const int kpb = kWaves * (64 / (d / 16)) * kKeys;
     const int nh = fa_heads_per_wg(hq, hkv);
     const long wgs_per_split = long(batch) * hkv * (hq / hkv / nh) * seq_q;
-    long want = (1024 + wgs_per_split - 1) / wgs_per_split;
-    const long max_by_len = (seq_kv + 63) / 64;
+    long want = (P1X_FA_TARGET_WGS + wgs_per_split - 1) / wgs_per_split;
+    const long max_by_len = (seq_kv + kpb - 1) / kpb;
     want = want < 1 ? 1 : want;
     want = want > max_by_len ? max_by_len : want;
     want = want > kMaxSplits ? kMaxSplits : want;
     chunk = int((seq_kv + want - 1) / want);
-    chunk = (chunk + 15) / 16 * 16;
+    chunk = (chunk + kpb - 1) / kpb * kpb;
     splits = (seq_kv + chunk - 1) / chunk;
 }
 
-hipError_t launch_fa_decode(FaArgs a, int batch, int d, float* o, float* lse, hipStream_t stream) {
+hipError_t launch_fa_decode(FaArgs a, int batch, int d, hipStream_t stream) {
     const int nh = fa_heads_per_wg(a.hq, a.hkv);
     a.head_chunks = (a.hq / a.hkv) / nh;
     switch (d) {
-        case 64: return launch_d<64>(a, batch, nh, o, lse, stream);
-        case 128: return launch_d<128>(a, batch, nh, o, lse, stream);
-        case 256: return launch_d<256>(a, batch, nh, o, lse, stream);
+        case 64: return launch_d<64>(a, batch, nh, stream);
+        case 128: return launch_d<128>(a, batch, nh, stream);
+        case 256: return launch_d<256>(a, batch, nh, stream);
     }
     return hipErrorInvalidValue;
 }

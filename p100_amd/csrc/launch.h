@@ -20,12 +20,16 @@ struct FaArgs {
     const __half* k;
     const __half* v;
     const float* mask;
-    float* part;  // [rows][splits][D + 2]: unnormalised O, base-2 max, sum
+    float* part_o;    // [groups][splits][NH][D]: unnormalised O of each split
+    float2* part_ml;  // [groups][splits][NH]: base-2 max and sum of each split
+    float* o;
+    float* lse;
     int64_t k_row, k_head, k_batch, v_row, v_head, v_batch;  // element strides
     int hq, hkv, seq_q, seq_kv, causal, splits, chunk, head_chunks;
     float scale, softcap;
 };
-hipError_t launch_fa_decode(FaArgs a, int batch, int d, float* o, float* lse, hipStream_t stream);
-void fa_split_plan(int batch, int hq, int hkv, int seq_q, int seq_kv, int& splits, int& chunk);
+hipError_t launch_fa_decode(FaArgs a, int batch, int d, hipStream_t stream);
+int fa_heads_per_wg(int hq, int hkv);
+void fa_split_plan(int batch, int hq, int hkv, int seq_q, int seq_kv, int d, int& splits, int& chunk);
 
 }  // namespace p1x

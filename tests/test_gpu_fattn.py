@@ -129,6 +129,57 @@ def test_softcap_and_large_logits(orc, gpu):
     check(orc, p, q, k, v)
 
 
+def test_workspace_reuse_and_graph_replay(orc, gpu):
+    """One workspace serves a sequence of different calls and replays of a captured graph (two launches per
+    call, the second reading the partials the first wrote), with eager calls between replays."""
+    import p100_amd as P
+    import torch
+
+    cfgs = [orc.AttnParams(n_head_q=32, n_head_kv=8, seq_q=1, seq_kv=8192, d_qk=128, d_v=128, causal=True),
+            orc.AttnParams(batch=2, n_head_q=6, n_head_kv=2, seq_q=3, seq_kv=300, d_qk=64, d_v=64, causal=True),
+            orc.AttnParams(n_head_q=8, n_head_kv=8, seq_q=1, seq_kv=2000, d_qk=256, d_v=256)]
+    need = max(P.flash_attn_decode_workspace(P._params(p)) for p in cfgs)
+    ws = torch.full((need // 4 + 4,), float("nan"), dtype=torch.float32, device="cuda")  # contents arbitrary
+    data = []
+    for n, p in enumerate(cfgs):
+        q, k, v = gen(orc, p, 500 + n)
+        qd, kd, vd = to_dev(q), to_dev(k.view(np.int16)).view(torch.float16), to_dev(v.view(np.int16)).view(torch.float16)
+        o = torch.empty(q.size, dtype=torch.float32, device="cuda")
+        lse = torch.empty(p.batch * p.n_head_q * p.seq_q, dtype=torch.float32, device="cuda")
+        data.append((P._params(p), qd, kd, vd, o, lse))
+    eager = []
+    for _ in range(2):  # each call twice, interleaved: results must not depend on what ran before
+        for p, qd, kd, vd, o, lse in data:
+            P.flash_attn_decode(p, qd, kd, vd, out=o, lse=lse, workspace=ws)
+            eager.append((o.clone(), lse.clone()))
+    for n in range(3):
+        assert torch.equal(eager[n][0], eager[n + 3][0]) and torch.equal(eager[n][1], eager[n + 3][1])
+    for (p, qd, kd, vd, o, lse), n in zip(data, range(3)):  # and they are right
+        q = qd.cpu().numpy()
+        ref, ref_lse = orc.attention_reference(cfgs[n], q, kd.cpu().numpy().astype(np.float32),
+                                               vd.cpu().numpy().astype(np.float32))
+        err = np.abs(eager[n][0].cpu().numpy().astype(np.float64) - ref)
+        assert (err <= 1e-3 + 2e-3 * np.abs(ref)).all()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            for p, qd, kd, vd, o, lse in data:
+                P.flash_attn_decode(p, qd, kd, vd, out=o, lse=lse, workspace=ws, stream=side)
+    for rep in range(3):
+        for _, _, _, _, o, lse in data:
+            o.fill_(float("nan"))
+            lse.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for n, (_, _, _, _, o, lse) in enumerate(data):
+            assert torch.equal(o, eager[n][0]) and torch.equal(lse, eager[n][1]), (rep, n)
+        P.flash_attn_decode(data[1][0], *data[1][1:4], out=data[1][4], lse=data[1][5], workspace=ws)  # eager between
+        torch.cuda.synchronize()
+
+
 def test_strided_kv_view(orc, gpu):
     """K and V as views into a larger cache: [batch][head][capacity][d] with capacity > seq_kv, and a row pitch."""
     import p100_amd as P
