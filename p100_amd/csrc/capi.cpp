@@ -230,6 +230,12 @@ int p1x_flash_attn_decode(const p1x_attn_params* p, const float* q, const uint16
         a.k_head = a.v_head = d * p->seq_kv;
         a.k_batch = a.v_batch = d * p->seq_kv * p->n_head_kv;
     }
+    // Bytes spanned by one head's seq_kv rows (the kernels' buffer range): 32-bit offsets.
+    const int64_t k_span = ((int64_t(p->seq_kv) - 1) * a.k_row + d) * 2, v_span = ((int64_t(p->seq_kv) - 1) * a.v_row + d) * 2;
+    if (k_span > 0x7ffffff0 || v_span > 0x7ffffff0)
+        return fail(P1X_EUNSUPPORTED, "one head's K or V rows must span less than 2 GiB");
+    a.k_bytes = uint32_t(k_span);
+    a.v_bytes = uint32_t(v_span);
     a.hq = p->n_head_q;
     a.hkv = p->n_head_kv;
     a.seq_q = p->seq_q;

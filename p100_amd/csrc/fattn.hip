@@ -6,19 +6,23 @@
 // per-tile FP16 VKQ flush, patch 0004, exists only because its TILE kernel accumulates in FP16).
 //
 // Pass 1 (k_fa_split): one 256-thread work-group per (split of the KV range, KV head, chunk of NH query heads
-// sharing it, query row). A key row is owned by LPK = D/16 lanes, 16 dimensions each (the two 8-element halves
-// [8l, 8l+8) and [D/2 + 8l, D/2 + 8l + 8), so one load instruction reads whole 128-byte lines of GPW = 64/LPK
-// consecutive rows). Each group of LPK lanes takes kKeys keys per batch; a batch's K and V loads are issued one
-// batch ahead of its arithmetic (two register buffers), with non-temporal hints since no element is read twice.
+// sharing it, query row). A key row is owned by LPK = D/8 lanes, 8 consecutive dimensions (one 16-byte load)
+// each, so one load instruction reads GPW = 64/LPK whole consecutive rows. Each group of LPK lanes takes kKeys
+// keys per batch; a batch's K and V loads are issued PF batches ahead of its arithmetic (a ring of register
+// buffers) as buffer loads, with non-temporal hints since no element is read twice; the buffer range check
+// lets loads past the share be issued unconditionally, which keeps every wait exact. Few registers per lane (8 Q and 8 O
+// columns per head) keep several waves per SIMD resident, which is what hides HBM latency here.
 // Softmax: each wave keeps one reference max per head, shared by its groups, and raises it (rescaling the sums,
 // a wave-uniform branch) only when a logit exceeds it by more than kTau, so after the first batch it rarely
 // moves; probabilities are 2^(x - ref) <= 2^kTau, and the groups' partial sums merge by plain addition (DPP
-// row rotation inside each 16-lane row, then LDS across rows and waves); the work-group writes one
-// unnormalised partial (O, max, sum) per head.
+// inside a 16-lane row, then LDS across rows and waves); the work-group writes one unnormalised partial
+// (O, max, sum) per head.
 // Pass 2 (k_fa_combine): one wave per output row rebases every split's partial to the common max and sums
 // (one round of loads per 32 splits). With a single split, pass 1 writes O and LSE itself and pass 2 is skipped.
-// (A single-launch variant, where the last work-group to arrive combines after an agent-scope release/acquire
-// pair, measured 2.4x slower at ctx 8192: each agent-scope release writes back the XCD's L2.)
+// (A single launch, where the last work-group to arrive combines, needs an agent-scope release per work-group:
+// each one writes back the XCD's L2, and one per work-group alone costs more than the second launch.)
+#include <type_traits>
+
 #include "common.h"
 #include "launch.h"
 
@@ -34,16 +38,35 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
-constexpr int kKeys = 2;         // keys per group per batch
+#ifndef P1X_FA_KEYS
+#define P1X_FA_KEYS 4  // keys per lane group per batch
+#endif
+#ifndef P1X_FA_MAX_NH
+#define P1X_FA_MAX_NH 2  // query heads per work-group, at most
+#endif
+constexpr int kKeys = P1X_FA_KEYS;
+#ifndef P1X_FA_DPL
+#define P1X_FA_DPL 8  // K/V dimensions per lane (8 or 16)
+#endif
+constexpr int kDimsPerLane = P1X_FA_DPL;
 constexpr int kWaves = 4;        // waves per pass-1 work-group
 constexpr int kMaxSplits = 256;  // fa_split_plan never exceeds this
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ uint4 ld_stream(const __half* p) {  // 16-byte load, non-temporal (read once)
-    const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-    return make_uint4(t.x, t.y, t.z, t.w);
+#ifndef P1X_FA_AUX
+#define P1X_FA_AUX 2  // buffer-load cache policy: non-temporal (each K/V element is read once)
+#endif
+// K/V rows of one (batch, KV head) through a buffer resource: the hardware range check turns any offset at or
+// past `bytes` into a load of zeros that touches no memory, so loads can be issued unconditionally.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t kv_rsrc(const __half* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<__half*>(base), (short)0, (int)bytes, 0x00020000);
 }
+__device__ __forceinline__ uint4 ld_kv(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, P1X_FA_AUX);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+constexpr uint32_t kOutOfRange = 0x7ffffff0u;  // an offset past every resource: loads return zeros
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
@@ -52,19 +75,21 @@ __device__ __forceinline__ float dpp_f(float v) {
 // DPP controls: quad_perm(1,0,3,2) = xor 1, quad_perm(2,3,0,1) = xor 2, row_half_mirror, row_mirror.
 constexpr int kXor1 = 0xB1, kXor2 = 0x4E, kHalfMirror = 0x141, kMirror = 0x140;
 
-// Sum over the aligned group of W (4, 8 or 16) lanes that own one key row; every lane gets the total.
+// Sum over the aligned group of W (4, 8, 16 or 32) lanes that own one key row; every lane gets the total.
 template <int W>
 __device__ __forceinline__ float key_sum(float v) {
     v += dpp_f<kXor1>(v);
     v += dpp_f<kXor2>(v);
     if constexpr (W >= 8) v += dpp_f<kHalfMirror>(v);
     if constexpr (W >= 16) v += dpp_f<kMirror>(v);
+    if constexpr (W >= 32)  // lane ^ 16 inside each 32-lane half: ds_swizzle bit mode (and 0x1f, xor 0x10)
+        v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
     return v;
 }
 
-constexpr int kRor4 = 0x124, kRor8 = 0x128;  // DPP row_ror:4 and row_ror:8 (lane ^ 8 inside a 16-lane row)
+constexpr int kRor4 = 0x124, kRor8 = 0x128;  // DPP row_ror:4 / row_ror:8 inside a 16-lane row
 
-// Sum over the groups of one 16-lane row that share l = lane % LPK; every lane of the row gets its row's sum.
+// Sum over the groups of one 16-lane row that share l = lane % LPK (LPK < 16); every lane of the row gets it.
 template <int LPK>
 __device__ __forceinline__ float row_group_sum(float v) {
     if constexpr (LPK <= 8) v += dpp_f<kRor8>(v);
@@ -77,7 +102,8 @@ template <int LPK>
 __device__ __forceinline__ float wave_group_max(float v) {
     if constexpr (LPK <= 8) v = fmaxf(v, dpp_f<kRor8>(v));
     if constexpr (LPK <= 4) v = fmaxf(v, dpp_f<kRor4>(v));
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F)));
+    if constexpr (LPK <= 16)
+        v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F)));
     return fmaxf(v, __shfl_xor(v, 32));
 }
 
@@ -94,10 +120,14 @@ __device__ __forceinline__ void h8_to_f32(uint4 v, float* out) {
 // Logits may exceed the wave's reference max by up to 2^kTau before the reference is raised (p <= 2^8).
 constexpr float kTau = 8.0f;
 
-template <int D, int NH>
+// MODE bit 0: additive mask; bit 1: logit softcap. Compile-time, so the plain decode loop carries neither.
+template <int D, int NH, int MODE>
 __global__ __launch_bounds__(256) void k_fa_split(FaArgs a) {
-    constexpr int LPK = D / 16;     // lanes per key row
-    constexpr int GPW = 64 / LPK;   // key groups per wave
+    constexpr bool kMask = (MODE & 1) != 0, kCap = (MODE & 2) != 0;
+    constexpr int DPL = kDimsPerLane;   // dimensions per lane: DPL/8 chunks of 8 (one 16-byte load each)
+    constexpr int CH = DPL / 8;
+    constexpr int LPK = D / DPL;        // lanes per key row
+    constexpr int GPW = 64 / LPK;       // key groups per wave
     constexpr int KPB = kWaves * GPW * kKeys;  // keys per work-group batch
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane / LPK, l = lane % LPK;
@@ -106,118 +136,124 @@ __global__ __launch_bounds__(256) void k_fa_split(FaArgs a) {
     const int b = kvh_all / a.hkv, kvh = kvh_all % a.hkv;
     const int i = blockIdx.z;
     const int h0 = kvh * (a.hq / a.hkv) + hc * NH;
+    // Chunk c of this lane holds dimensions [c*D/CH + 8l, c*D/CH + 8l + 8): each load instruction of a wave
+    // covers the same 1/CH slice of GPW consecutive rows (whole 128-byte lines).
+    auto dim0 = [&](int c) { return c * (D / CH) + 8 * l; };
 
     // Visible keys [0, j_end); this work-group's share [j0, j1).
     const int j_end = a.causal ? min(a.seq_kv, i + (a.seq_kv - a.seq_q) + 1) : a.seq_kv;
     const int j0 = split * a.chunk;
     const int j1 = min(j0 + a.chunk, j_end);
 
-    const bool cap = a.softcap > 0.0f;
-    const float qmul = cap ? a.scale : a.scale * kLog2e;
-    float qr[NH][16];
+    const float qmul = kCap ? a.scale : a.scale * kLog2e;
+    float qr[NH][DPL];
 #pragma unroll
     for (int hh = 0; hh < NH; ++hh) {
-        const float* qp = a.q + ((size_t(b) * a.hq + h0 + hh) * a.seq_q + i) * D + 8 * l;
+        const float* qp = a.q + ((size_t(b) * a.hq + h0 + hh) * a.seq_q + i) * D;
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const float4 x0 = *reinterpret_cast<const float4*>(qp + half * (D / 2));
-            const float4 x1 = *reinterpret_cast<const float4*>(qp + half * (D / 2) + 4);
-            float* r = qr[hh] + 8 * half;
+        for (int c = 0; c < CH; ++c) {
+            const float4 x0 = *reinterpret_cast<const float4*>(qp + dim0(c));
+            const float4 x1 = *reinterpret_cast<const float4*>(qp + dim0(c) + 4);
+            float* r = qr[hh] + 8 * c;
             r[0] = x0.x * qmul; r[1] = x0.y * qmul; r[2] = x0.z * qmul; r[3] = x0.w * qmul;
             r[4] = x1.x * qmul; r[5] = x1.y * qmul; r[6] = x1.z * qmul; r[7] = x1.w * qmul;
         }
     }
     // Softmax state: a wave-uniform reference max per head, and per-lane partial sums (group-local keys).
-    float mref[NH], s[NH], o[NH][16];
+    float mref[NH], s[NH], o[NH][DPL];
 #pragma unroll
     for (int hh = 0; hh < NH; ++hh) {
         mref[hh] = -INFINITY;
         s[hh] = 0.0f;
 #pragma unroll
-        for (int d = 0; d < 16; ++d) o[hh][d] = 0.0f;
+        for (int d = 0; d < DPL; ++d) o[hh][d] = 0.0f;
     }
-    const __half* kb = a.k + size_t(b) * a.k_batch + size_t(kvh) * a.k_head + 8 * l;
-    const __half* vb = a.v + size_t(b) * a.v_batch + size_t(kvh) * a.v_head + 8 * l;
-    const float* mrow = a.mask ? a.mask + size_t(i) * a.seq_kv : nullptr;
+    const auto krs = kv_rsrc(a.k + size_t(b) * a.k_batch + size_t(kvh) * a.k_head, a.k_bytes);
+    const auto vrs = kv_rsrc(a.v + size_t(b) * a.v_batch + size_t(kvh) * a.v_head, a.v_bytes);
+    const float* mrow = kMask ? a.mask + size_t(i) * a.seq_kv : nullptr;
 
     // Key of (batch t, slot u) for this lane's group: the GPW groups of a wave read GPW consecutive rows.
+    // Only the last batch of the share can be partial (chunks are whole batches); it alone masks keys.
     const int nb = j1 > j0 ? (j1 - j0 + KPB - 1) / KPB : 0;
-    auto key_of = [&](int t, int u) { return j0 + t * KPB + (wave * kKeys + u) * GPW + g; };
+    const bool tail = nb > 0 && j0 + nb * KPB > j1;
+    const int key0 = j0 + wave * kKeys * GPW + g;  // slot u of batch t: key0 + t * KPB + u * GPW
     struct Buf {
-        uint4 k[kKeys][2], v[kKeys][2];
+        uint4 k[kKeys][CH], v[kKeys][CH];
     };
+    // Unconditional loads (batches past nb get out-of-range offsets), so the number of loads in flight is the
+    // same on every path and each wait covers exactly the batch about to be used.
     auto load = [&](Buf& bf, int t) {
 #pragma unroll
         for (int u = 0; u < kKeys; ++u) {
-            const int j = key_of(t, u);
-            const int jc = j < j1 ? j : j0;  // keys past the share reload a valid row; their logit becomes -inf
-            const __half* kr = kb + size_t(jc) * a.k_row;
-            const __half* vr = vb + size_t(jc) * a.v_row;
-            bf.k[u][0] = ld_stream(kr);
-            bf.k[u][1] = ld_stream(kr + D / 2);
-            bf.v[u][0] = ld_stream(vr);
-            bf.v[u][1] = ld_stream(vr + D / 2);
+            const uint32_t j = uint32_t(key0 + t * KPB + u * GPW);
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                bf.k[u][c] = ld_kv(krs, t < nb ? (j * uint32_t(a.k_row) + dim0(c)) * 2 : kOutOfRange);
+                bf.v[u][c] = ld_kv(vrs, t < nb ? (j * uint32_t(a.v_row) + dim0(c)) * 2 : kOutOfRange);
+            }
         }
     };
-    auto compute = [&](const Buf& bf, int t) {
+    auto compute = [&](const Buf& bf, int t, auto last_tag) {
+        constexpr bool kLast = decltype(last_tag)::value;
         float x[kKeys][NH];
 #pragma unroll
         for (int u = 0; u < kKeys; ++u) {
-            float kf[16];
-            h8_to_f32(bf.k[u][0], kf);
-            h8_to_f32(bf.k[u][1], kf + 8);
+            float kf[DPL];
+#pragma unroll
+            for (int c = 0; c < CH; ++c) h8_to_f32(bf.k[u][c], kf + 8 * c);
 #pragma unroll
             for (int hh = 0; hh < NH; ++hh) {
                 float d0 = 0.0f, d1 = 0.0f;
 #pragma unroll
-                for (int d = 0; d < 8; ++d) {
+                for (int d = 0; d < DPL / 2; ++d) {
                     d0 = fmaf(qr[hh][d], kf[d], d0);
-                    d1 = fmaf(qr[hh][8 + d], kf[8 + d], d1);
+                    d1 = fmaf(qr[hh][DPL / 2 + d], kf[DPL / 2 + d], d1);
                 }
                 x[u][hh] = key_sum<LPK>(d0 + d1);
             }
-            const int j = key_of(t, u);
-            const bool ok = j < j1;
-            if (cap || mrow) {
-                const float add = (mrow && ok) ? mrow[j] : 0.0f;
+            const int j = key0 + t * KPB + u * GPW;
+            const bool ok = !kLast || j < j1;
+            if constexpr (kMask || kCap) {
+                const float add = kMask && ok ? mrow[j] : 0.0f;
 #pragma unroll
                 for (int hh = 0; hh < NH; ++hh)
-                    x[u][hh] = cap ? (a.softcap * tanhf(x[u][hh] / a.softcap) + add) * kLog2e : x[u][hh] + add * kLog2e;
+                    x[u][hh] = kCap ? (a.softcap * tanhf(x[u][hh] / a.softcap) + add) * kLog2e : x[u][hh] + add * kLog2e;
             }
+            if constexpr (kLast) {
 #pragma unroll
-            for (int hh = 0; hh < NH; ++hh) x[u][hh] = ok ? x[u][hh] : -INFINITY;
+                for (int hh = 0; hh < NH; ++hh) x[u][hh] = ok ? x[u][hh] : -INFINITY;
+            }
         }
-        bool need = false;
+        // Raise the references only when some logit exceeds its head's by more than kTau (x - (-inf) = +inf
+        // forces the first raise; -inf - (-inf) = NaN is ignored by fmaxf).
+        float over = -INFINITY;
 #pragma unroll
         for (int hh = 0; hh < NH; ++hh)
 #pragma unroll
-            for (int u = 0; u < kKeys; ++u) need |= x[u][hh] > mref[hh] + kTau;
-        if (__any(need)) {  // wave-uniform: raise the reference to the wave's max, rescaling what was summed
+            for (int u = 0; u < kKeys; ++u) over = fmaxf(over, x[u][hh] - mref[hh]);
+        if (__any(over > kTau)) {  // wave-uniform and rare: rescale every head to its new wave max
 #pragma unroll
             for (int hh = 0; hh < NH; ++hh) {
                 float bm = x[0][hh];
 #pragma unroll
                 for (int u = 1; u < kKeys; ++u) bm = fmaxf(bm, x[u][hh]);
-                bm = wave_group_max<LPK>(bm);  // the same value in every lane
-                const float mn = fmaxf(mref[hh], bm);
-                if (mn > mref[hh]) {
-                    const float alpha = mref[hh] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mref[hh] - mn);
-                    s[hh] *= alpha;
+                const float mn = fmaxf(mref[hh], wave_group_max<LPK>(bm));  // the same value in every lane
+                const float alpha = mref[hh] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mref[hh] - mn);
+                s[hh] *= alpha;
 #pragma unroll
-                    for (int d = 0; d < 16; ++d) o[hh][d] *= alpha;
-                    mref[hh] = mn;
-                }
+                for (int d = 0; d < DPL; ++d) o[hh][d] *= alpha;
+                mref[hh] = mn;
             }
         }
-        float vf[kKeys][16];
+        float vf[kKeys][DPL];
 #pragma unroll
-        for (int u = 0; u < kKeys; ++u) {
-            h8_to_f32(bf.v[u][0], vf[u]);
-            h8_to_f32(bf.v[u][1], vf[u] + 8);
-        }
+        for (int u = 0; u < kKeys; ++u)
+#pragma unroll
+            for (int c = 0; c < CH; ++c) h8_to_f32(bf.v[u][c], vf[u] + 8 * c);
 #pragma unroll
         for (int hh = 0; hh < NH; ++hh) {
-            const float base = mref[hh] == -INFINITY ? 0.0f : mref[hh];  // all keys so far masked: p = 0
+            // Masks can leave every key so far at -inf: then the reference is -inf and p must be 0.
+            const float base = (kMask || kLast) && mref[hh] == -INFINITY ? 0.0f : mref[hh];
             float p[kKeys];
 #pragma unroll
             for (int u = 0; u < kKeys; ++u) {
@@ -225,7 +261,7 @@ __global__ __launch_bounds__(256) void k_fa_split(FaArgs a) {
                 s[hh] += p[u];
             }
 #pragma unroll
-            for (int d = 0; d < 16; ++d) {
+            for (int d = 0; d < DPL; ++d) {
                 float acc = o[hh][d];
 #pragma unroll
                 for (int u = 0; u < kKeys; ++u) acc = fmaf(p[u], vf[u][d], acc);
@@ -234,44 +270,53 @@ __global__ __launch_bounds__(256) void k_fa_split(FaArgs a) {
         }
     };
 
-    // A ring of PF register buffers: batch t + PF is requested as soon as batch t has been consumed.
+    // A ring of PF register buffers: batch t + PF is requested as soon as batch t has been consumed. Whole
+    // blocks of PF batches run with loads; the remaining nb % PF batches were already requested.
     constexpr int PF = P1X_FA_PF;
+    auto step = [&](Buf& bf, int t) {
+        if (tail && t == nb - 1) compute(bf, t, std::true_type{});
+        else compute(bf, t, std::false_type{});
+    };
     Buf ring[PF];
 #pragma unroll
-    for (int p = 0; p < PF; ++p)
-        if (p < nb) load(ring[p], p);
-    for (int t0 = 0; t0 < nb; t0 += PF) {
+    for (int p = 0; p < PF; ++p) load(ring[p], p);
+    int t0 = 0;
+    for (; t0 + PF <= nb; t0 += PF) {
 #pragma unroll
         for (int p = 0; p < PF; ++p) {
-            const int t = t0 + p;
-            if (t >= nb) break;
-            compute(ring[p], t);
-            if (t + PF < nb) load(ring[p], t + PF);
+            step(ring[p], t0 + p);
+            load(ring[p], t0 + p + PF);
         }
     }
+#pragma unroll
+    for (int p = 0; p < PF - 1; ++p)
+        if (t0 + p < nb) step(ring[p], t0 + p);
 
-    // The groups of a wave share its reference max, so their partial sums merge by plain addition: inside each
-    // 16-lane row with DPP, then the 4 rows of each of the 4 waves through LDS.
+    // The groups of a wave share its reference max, so their partial sums merge by plain addition: the groups
+    // of one 16-lane row with DPP rotations, then through LDS, one state per 16-lane row (or per group when a
+    // group spans two rows), across the 4 waves.
+    if constexpr (LPK < 16) {
 #pragma unroll
-    for (int hh = 0; hh < NH; ++hh) {
-        s[hh] = row_group_sum<LPK>(s[hh]);
+        for (int hh = 0; hh < NH; ++hh) {
+            s[hh] = row_group_sum<LPK>(s[hh]);
 #pragma unroll
-        for (int d = 0; d < 16; ++d) o[hh][d] = row_group_sum<LPK>(o[hh][d]);
+            for (int d = 0; d < DPL; ++d) o[hh][d] = row_group_sum<LPK>(o[hh][d]);
+        }
     }
-    constexpr int kStates = kWaves * 4;  // one per 16-lane row
-    __shared__ float wm[kWaves][NH], wsum[kStates][NH];
-    __shared__ float wo[kStates][NH][D];
-    const int row16 = lane >> 4, st = wave * 4 + row16;
-    if ((lane & 15) < LPK) {  // the first group of each row holds the row's sums; l = lane & 15 there
+    constexpr int RPG = LPK > 16 ? LPK / 16 : 1;  // 16-lane rows per group
+    constexpr int SPW = 4 / RPG;                  // states per wave
+    __shared__ float wm[kWaves][NH], wsum[kWaves * SPW][NH];
+    __shared__ float wo[kWaves * SPW][NH][D];
+    const int st = wave * SPW + (lane >> 4) / RPG;
+    if (LPK >= 16 || (lane & 15) < LPK) {  // one group per state writes it (l = lane % LPK)
 #pragma unroll
         for (int hh = 0; hh < NH; ++hh) {
             if (lane == 0) wm[wave][hh] = mref[hh];
             if (l == 0) wsum[st][hh] = s[hh];
 #pragma unroll
-            for (int d = 0; d < 8; ++d) {
-                wo[st][hh][8 * l + d] = o[hh][d];
-                wo[st][hh][D / 2 + 8 * l + d] = o[hh][8 + d];
-            }
+            for (int c = 0; c < CH; ++c)
+#pragma unroll
+                for (int d = 0; d < 8; ++d) wo[st][hh][dim0(c) + d] = o[hh][8 * c + d];
         }
     }
     __syncthreads();
@@ -290,9 +335,9 @@ __global__ __launch_bounds__(256) void k_fa_split(FaArgs a) {
             const float wt = wm[w][hh] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(wm[w][hh] - mx);
             float n = 0.0f, sm = 0.0f;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                n += wo[w * 4 + r][hh][d];
-                sm += wsum[w * 4 + r][hh];
+            for (int r = 0; r < SPW; ++r) {
+                n += wo[w * SPW + r][hh][d];
+                sm += wsum[w * SPW + r][hh];
             }
             num = fmaf(wt, n, num);
             den = fmaf(wt, sm, den);
@@ -307,8 +352,6 @@ __global__ __launch_bounds__(256) void k_fa_split(FaArgs a) {
             if (d == 0) a.part_ml[pr] = make_float2(mx, den);
         }
     }
-    if (a.splits == 1) return;
-
 }
 
 // Wave max / sum over all 64 lanes (every lane gets the result): DPP inside rows, then swizzle and bpermute.
@@ -412,7 +455,12 @@ __global__ __launch_bounds__(256) void k_fa_combine(FaArgs a, int rows) {
 template <int D, int NH>
 hipError_t launch_split(const FaArgs& a, int batch, hipStream_t stream) {
     const dim3 grid(a.splits, batch * a.hkv * a.head_chunks, a.seq_q);
-    hipLaunchKernelGGL((k_fa_split<D, NH>), grid, dim3(256), 0, stream, a);
+    switch ((a.mask ? 1 : 0) | (a.softcap > 0.0f ? 2 : 0)) {
+        case 0: hipLaunchKernelGGL((k_fa_split<D, NH, 0>), grid, dim3(256), 0, stream, a); break;
+        case 1: hipLaunchKernelGGL((k_fa_split<D, NH, 1>), grid, dim3(256), 0, stream, a); break;
+        case 2: hipLaunchKernelGGL((k_fa_split<D, NH, 2>), grid, dim3(256), 0, stream, a); break;
+        default: hipLaunchKernelGGL((k_fa_split<D, NH, 3>), grid, dim3(256), 0, stream, a); break;
+    }
     if (a.splits == 1) return hipGetLastError();  // the split pass wrote O and LSE
     const int rows = batch * a.hq * a.seq_q;
     hipLaunchKernelGGL((k_fa_combine<D, NH>), dim3((rows + kWaves - 1) / kWaves), dim3(256), 0, stream, a, rows);
@@ -435,14 +483,14 @@ hipError_t launch_d(const FaArgs& a, int batch, int nh, hipStream_t stream) {
 int fa_heads_per_wg(int hq, int hkv) {
     const int group = hq / hkv;
     for (int nh : {4, 2, 1})
-        if (group % nh == 0) return nh;
+        if (nh <= P1X_FA_MAX_NH && group % nh == 0) return nh;
     return 1;
 }
 
 // KV split: chunks of whole work-group batches (4 waves x 64/(d/16) groups x 2 keys), about
 // P1X_FA_TARGET_WGS pass-1 work-groups in total, at most kMaxSplits splits.
 void fa_split_plan(int batch, int hq, int hkv, int seq_q, int seq_kv, int d, int& splits, int& chunk) {
-    const int kpb = kWaves * (64 / (d / 16)) * kKeys;
+    const int kpb = kWaves * (64 / (d / kDimsPerLane)) * kKeys;
     const int nh = fa_heads_per_wg(hq, hkv);
     const long wgs_per_split = long(batch) * hkv * (hq / hkv / nh) * seq_q;
     long want = (P1X_FA_TARGET_WGS + wgs_per_split - 1) / wgs_per_split;

@@ -25,6 +25,7 @@ struct FaArgs {
     float* o;
     float* lse;
     int64_t k_row, k_head, k_batch, v_row, v_head, v_batch;  // element strides
+    uint32_t k_bytes, v_bytes;  // bytes spanned by one head's seq_kv rows of K and of V
     int hq, hkv, seq_q, seq_kv, causal, splits, chunk, head_chunks;
     float scale, softcap;
 };
