@@ -128,9 +128,9 @@ int p1x_prepare_h16(const float* x, uint16_t* h, float* meta, int64_t K, int64_t
 
 size_t p1x_mul_mat_vec_workspace(int wtype, int64_t M, int64_t K, int64_t ncols, int act_mode) {
     (void)wtype;
-    (void)M;
-    if (K <= 0 || ncols <= 0) return 0;
-    return act_mode == P1X_ACT_H16 ? h16_bytes(K, ncols) : q8_1_bytes(K, ncols);
+    if (K <= 0 || ncols <= 0 || M <= 0) return 0;
+    if (act_mode == P1X_ACT_H16) return h16_bytes(K, ncols);
+    return K <= INT32_MAX && M <= INT32_MAX && p1x::mmvq_fused_fits(int(ncols), int(M), int(K)) ? 0 : q8_1_bytes(K, ncols);
 }
 
 int p1x_mul_mat_vec_q8_1(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K, const int8_t* qs,
@@ -139,7 +139,7 @@ int p1x_mul_mat_vec_q8_1(int wtype, const void* w, int64_t nb01, int64_t M, int6
     if (int rc = check_matvec(wtype, w, nb01, M, K, ncols, y)) return rc;
     if (!qs || !ds) return fail(P1X_EINVAL, "null activation pointer");
     if (!aligned(qs, 16) || !aligned(ds, 16)) return fail(P1X_EINVAL, "qs and ds must be 16-byte aligned");
-    hipError_t e = p1x::launch_mmvq(wtype, int(ncols), w, nb01, int(M), int(K), qs, ds, y, group_sums,
+    hipError_t e = p1x::launch_mmvq(wtype, int(ncols), w, nb01, int(M), int(K), qs, ds, nullptr, y, group_sums,
                                     static_cast<hipStream_t>(stream));
     return e == hipSuccess ? P1X_OK : hip_fail(e, "mul_mat_vec_q8_1");
 }
@@ -164,17 +164,23 @@ int p1x_mul_mat_vec(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K
     if (act_mode == P1X_ACT_H16 && group_sums)
         return fail(P1X_EINVAL, "group sums exist only for the Q8_1 activation mode");
     const size_t need = p1x_mul_mat_vec_workspace(wtype, M, K, ncols, act_mode);
-    if (!ws || ws_bytes < need)
+    if (need && (!ws || ws_bytes < need))
         return fail(P1X_EWORKSPACE, "workspace of " + std::to_string(need) + " bytes required");
-    if (!aligned(ws, 256)) return fail(P1X_EINVAL, "workspace must be 256-byte aligned");
+    if (need && !aligned(ws, 256)) return fail(P1X_EINVAL, "workspace must be 256-byte aligned");
     auto* base = static_cast<uint8_t*>(ws);
     const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (act_mode == P1X_ACT_Q8_1 && need == 0) {  // one launch: the kernel quantizes x itself
+        if (!aligned(x, 16)) return fail(P1X_EINVAL, "x must be 16-byte aligned");
+        hipError_t e = p1x::launch_mmvq(wtype, int(ncols), w, nb01, int(M), int(K), nullptr, nullptr, x, y,
+                                        group_sums, s);
+        return e == hipSuccess ? P1X_OK : hip_fail(e, "mul_mat_vec");
+    }
     if (act_mode == P1X_ACT_Q8_1) {
         auto* qs = reinterpret_cast<int8_t*>(base);
         auto* ds = reinterpret_cast<float*>(base + align256(size_t(K) * ncols));
         hipError_t e = p1x::launch_quantize_q8_1(x, qs, ds, int(K), int(ncols), s);
         if (e != hipSuccess) return hip_fail(e, "quantize_q8_1");
-        e = p1x::launch_mmvq(wtype, int(ncols), w, nb01, int(M), int(K), qs, ds, y, group_sums, s);
+        e = p1x::launch_mmvq(wtype, int(ncols), w, nb01, int(M), int(K), qs, ds, nullptr, y, group_sums, s);
         return e == hipSuccess ? P1X_OK : hip_fail(e, "mul_mat_vec_q8_1");
     }
     auto* h = reinterpret_cast<uint16_t*>(base);

@@ -16,7 +16,18 @@ enum WType { Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q6_K = 14 };
 struct __attribute__((aligned(4))) U32x4 {
     uint32_t x, y, z, w;
 };
-__device__ __forceinline__ U32x4 ld_u32x4(const uint32_t* p) { return *reinterpret_cast<const U32x4*>(p); }
+// Weight pointers are rebuilt from integer addresses (dword rounding), which loses the address space: these
+// helpers put them back in the global one, so loads are global_load_* rather than flat_load_* (flat loads also
+// count against lgkmcnt, which would make every LDS wait wait for the weight stream too).
+typedef __attribute__((address_space(1))) const uint32_t gu32;
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4), aligned(4)));
+typedef __attribute__((address_space(1))) const u32x4v gu32x4;
+__device__ __forceinline__ const gu32* global_dwords(uintptr_t a) { return (const gu32*)a; }
+__device__ __forceinline__ const gu32* global_dwords(const void* p) { return global_dwords(reinterpret_cast<uintptr_t>(p)); }
+__device__ __forceinline__ U32x4 ld_u32x4(const gu32* p) {
+    const u32x4v v = *(const gu32x4*)p;
+    return U32x4{v.x, v.y, v.z, v.w};
+}
 
 // Packed signed int8 dot product with int32 accumulate: v_dot4_i32_i8 (exact).
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
@@ -35,7 +46,7 @@ __device__ __forceinline__ uint32_t slice_sel(uint32_t shift) { return shift ? 0
 // block: a read never leaves the block's pages. q receives the quant bytes re-sliced to dwords, d the fp16 bits.
 __device__ __forceinline__ void load_q4_0_block(const uint8_t* p, uint32_t q[4], uint32_t& d) {
     const uintptr_t addr = reinterpret_cast<uintptr_t>(p);
-    const uint32_t* base = reinterpret_cast<const uint32_t*>(addr & ~uintptr_t(3));
+    const gu32* base = global_dwords(addr & ~uintptr_t(3));
     const uint32_t sh = uint32_t(addr & 2);
     const U32x4 v = ld_u32x4(base);
     const uint32_t w4 = base[4];
@@ -48,7 +59,7 @@ __device__ __forceinline__ void load_q4_0_block(const uint8_t* p, uint32_t q[4],
 }
 __device__ __forceinline__ void load_q8_0_block(const uint8_t* p, uint32_t q[8], uint32_t& d) {
     const uintptr_t addr = reinterpret_cast<uintptr_t>(p);
-    const uint32_t* base = reinterpret_cast<const uint32_t*>(addr & ~uintptr_t(3));
+    const gu32* base = global_dwords(addr & ~uintptr_t(3));
     const uint32_t sh = uint32_t(addr & 2);
     const U32x4 v0 = ld_u32x4(base), v1 = ld_u32x4(base + 4);
     const uint32_t w[9] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w, base[8]};
@@ -63,7 +74,7 @@ __device__ __forceinline__ void load_q8_0_block(const uint8_t* p, uint32_t q[8],
 template <int N>
 __device__ __forceinline__ void load_field(const uint8_t* p, uint32_t* out) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t* base = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+    const gu32* base = global_dwords(a & ~uintptr_t(3));
     uint32_t w[N + 1];
 #pragma unroll
     for (int i = 0; i < N; i += 4) {
@@ -82,7 +93,7 @@ __device__ __forceinline__ void load_field(const uint8_t* p, uint32_t* out) {
 // The 16 bits at a 2-byte aligned address (a scale inside a block).
 __device__ __forceinline__ uint32_t load_u16(const uint8_t* p) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    return (*reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3)) >> (8 * (a & 2))) & 0xffffu;
+    return (*global_dwords(a & ~uintptr_t(3)) >> (8 * (a & 2))) & 0xffffu;
 }
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {

@@ -78,7 +78,7 @@ __device__ __forceinline__ Unpacked unpack(const uint8_t* row, int u) {
         }
     } else if constexpr (TYPE == Q4_K) {
         const int blk = u >> 3, s = u & 7;
-        const uint32_t* p = reinterpret_cast<const uint32_t*>(row + size_t(blk) * 144);
+        const gu32* p = global_dwords(row + size_t(blk) * 144);
         const U32x4 hdr = ld_u32x4(p);
         const U32x4 qa = ld_u32x4(p + 4 + 8 * (s >> 1)), qb = ld_u32x4(p + 8 + 8 * (s >> 1));
         const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};

@@ -26,9 +26,87 @@ struct ActBlock {  // one 32-element Q8_1 block: q[0..15], q[16..31], {d, s, isu
     float4 ds;
 };
 
-__device__ __forceinline__ ActBlock load_act(const int8_t* qs, const float4* ds, int K, int c, int blk) {
-    const int4* p = reinterpret_cast<const int4*>(qs + size_t(c) * K + size_t(blk) * 32);
-    return ActBlock{p[0], p[1], ds[size_t(c) * (K / 32) + blk]};
+// Activation sources: a Q8_1 activation prepared in global memory (p1x_quantize_q8_1's layout), or one the
+// work-group quantized itself into LDS (three arrays of 16-byte entries per block, so lanes reading
+// consecutive blocks hit consecutive banks).
+struct ActGlobal {
+    const int8_t* qs;
+    const float4* ds;
+    int K;
+    __device__ __forceinline__ ActBlock get(int c, int blk) const {
+        const int4* p = reinterpret_cast<const int4*>(qs + size_t(c) * K + size_t(blk) * 32);
+        return ActBlock{p[0], p[1], ds[size_t(c) * (K / 32) + blk]};
+    }
+};
+struct ActLds {
+    const uint4* lo;  // q[0..15] of block (c, b) at c * nblk + b
+    const uint4* hi;  // q[16..31]
+    const float4* ds;
+    int nblk;
+    __device__ __forceinline__ ActBlock get(int c, int blk) const {
+        const int i = c * nblk + blk;
+        return ActBlock{__builtin_bit_cast(int4, lo[i]), __builtin_bit_cast(int4, hi[i]), ds[i]};
+    }
+};
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, true);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
+}
+constexpr int kQuadXor1 = 0xB1, kQuadXor2 = 0x4E;  // quad_perm(1,0,3,2), quad_perm(2,3,0,1)
+
+// Q8_1 of B columns of x (f32 [B][K]) into LDS by the whole work-group. A 32-element block is held by a quad of
+// lanes, 8 consecutive elements each (lane t of the quad: elements 8t..8t+7). The arithmetic is that of
+// k_quantize_q8_1 (qmv_model.cpp:60-68): d = amax/127 and q = round(x/d) with IEEE division, and the sum s
+// follows the reference's xor butterfly exactly (offsets 16, 8: lanes ^ 2, ^ 1 of the quad; 4, 2, 1: inside
+// the lane), so the block is bit-identical to the standalone kernel's.
+template <int B>
+__device__ __forceinline__ void quantize_to_lds(const float* __restrict__ x, int K, uint4* lo, uint4* hi, float4* ds) {
+    const int nblk = K / 32, per_col = K / 8, nchunk = B * per_col;  // nchunk % 4 == 0: quads stay whole
+    for (int base = 0; base < nchunk; base += 256) {
+        const int ch = base + int(threadIdx.x);
+        const bool ok = ch < nchunk;
+        const int chc = ok ? ch : ch - ((ch - nchunk) / 4 + 1) * 4;  // past the end: a valid chunk, not stored
+        const int c = chc / per_col, e8 = chc - c * per_col;
+        const float4* src = reinterpret_cast<const float4*>(x + size_t(c) * K + size_t(e8) * 8);
+        const float4 a0 = src[0], a1 = src[1];
+        const float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        float m = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[e]));
+        m = fmaxf(m, dpp_f<kQuadXor1>(m));
+        m = fmaxf(m, dpp_f<kQuadXor2>(m));
+        const float d = m / 127.0f;
+        int q[8], isum = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            q[e] = m == 0.0f ? 0 : static_cast<int>(roundf(v[e] / d));
+            isum += q[e];
+        }
+        isum += dpp_i<kQuadXor1>(isum);
+        isum += dpp_i<kQuadXor2>(isum);
+        float t[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) t[e] = v[e] + dpp_f<kQuadXor2>(v[e]);  // offset 16 (element bit 4)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) t[e] = t[e] + dpp_f<kQuadXor1>(t[e]);  // offset 8 (bit 3)
+        const float w0 = t[0] + t[4], w1 = t[1] + t[5], w2 = t[2] + t[6], w3 = t[3] + t[7];  // offset 4
+        const float sum = (w0 + w2) + (w1 + w3);                                               // offsets 2, 1
+        if (ok) {
+            const int blk = c * nblk + (e8 >> 2), lt = e8 & 3;
+            const uint32_t p0 = (uint32_t(q[0]) & 255) | (uint32_t(q[1]) & 255) << 8 | (uint32_t(q[2]) & 255) << 16 |
+                                uint32_t(q[3]) << 24;
+            const uint32_t p1 = (uint32_t(q[4]) & 255) | (uint32_t(q[5]) & 255) << 8 | (uint32_t(q[6]) & 255) << 16 |
+                                uint32_t(q[7]) << 24;
+            uint2* dst = reinterpret_cast<uint2*>(lt < 2 ? &lo[blk] : &hi[blk]) + (lt & 1);
+            *dst = make_uint2(p0, p1);
+            if (lt == 0) ds[blk] = make_float4(round_fp16(d), round_fp16(sum), static_cast<float>(isum), 0.0f);
+        }
+    }
 }
 
 __device__ __forceinline__ int dot8(const uint32_t* w, int4 x0, int4 x1) {
@@ -54,7 +132,7 @@ struct UnitQ4_0 {
     uint32_t w[5], sh;
     __device__ __forceinline__ void load(const uint8_t* row, int u) {
         const uintptr_t a = reinterpret_cast<uintptr_t>(row + size_t(u) * 18);
-        const uint32_t* base = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+        const gu32* base = global_dwords(a & ~uintptr_t(3));
         const U32x4 v = ld_u32x4(base);  // reads only dwords holding block bytes (see common.h)
         w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
         w[4] = base[4];
@@ -82,7 +160,7 @@ struct UnitQ8_0 {
     uint32_t w[9], sh;
     __device__ __forceinline__ void load(const uint8_t* row, int u) {
         const uintptr_t a = reinterpret_cast<uintptr_t>(row + size_t(u) * 34);
-        const uint32_t* base = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+        const gu32* base = global_dwords(a & ~uintptr_t(3));
         const U32x4 v0 = ld_u32x4(base), v1 = ld_u32x4(base + 4);
         w[0] = v0.x; w[1] = v0.y; w[2] = v0.z; w[3] = v0.w;
         w[4] = v1.x; w[5] = v1.y; w[6] = v1.z; w[7] = v1.w;
@@ -121,7 +199,7 @@ struct UnitQ4_K {
     int g;
     __device__ __forceinline__ void load(const uint8_t* row, int u) {
         g = u & 3;
-        const uint32_t* p = reinterpret_cast<const uint32_t*>(row + size_t(u >> 2) * 144);  // 4-byte aligned
+        const gu32* p = global_dwords(row + size_t(u >> 2) * 144);  // 4-byte aligned
         const U32x4 h = ld_u32x4(p), qa = ld_u32x4(p + 4 + 8 * g), qb = ld_u32x4(p + 8 + 8 * g);
         hdr[0] = h.x; hdr[1] = h.y; hdr[2] = h.z; hdr[3] = h.w;
         q[0] = qa.x; q[1] = qa.y; q[2] = qa.z; q[3] = qa.w;
@@ -215,64 +293,102 @@ __device__ __forceinline__ float wave_total(float v) {
     return v;
 }
 
-template <int TYPE, int B, int RW, bool SUMS>
-__global__ __launch_bounds__(256) void k_mmvq(const uint8_t* __restrict__ w, int64_t nb01, int M, int K,
-                                              const int8_t* __restrict__ xq, const float4* __restrict__ xds,
-                                              float* __restrict__ y, int32_t* __restrict__ gs) {
+// Copy of a prepared Q8_1 activation (global, p1x_quantize_q8_1's layout) into the LDS layout of ActLds.
+template <int B>
+__device__ __forceinline__ void copy_to_lds(const int8_t* __restrict__ qs, const float4* __restrict__ ds, int K,
+                                            uint4* lo, uint4* hi, float4* dl) {
+    const int nblk = K / 32;
+    for (int i = threadIdx.x; i < B * nblk; i += 256) {
+        const int c = i / nblk, b = i - c * nblk;
+        const uint4* src = reinterpret_cast<const uint4*>(qs + size_t(c) * K + size_t(b) * 32);
+        lo[i] = src[0];
+        hi[i] = src[1];
+        dl[i] = ds[i];
+    }
+}
+
+// Rows r0 .. r0+RW-1 of one wave, pass by pass over K (64 UB units per pass). The weights of pass p+1 are
+// requested before pass p computes, with two register sets used alternately (the loop body is two passes), so
+// every load in the loop body is unconditional and each wait covers exactly the pass about to be used; the
+// last one or two passes run in an epilogue. `prep` runs first (quantize x into LDS, or copy a prepared
+// activation there); every wave, even one past the last row, takes part in it.
+template <int TYPE, int B, int RW, bool SUMS, class Act, class Prep>
+__device__ __forceinline__ void mmvq_rows(const Act act, Prep prep, const uint8_t* __restrict__ w, int64_t nb01,
+                                          int M, int K, float* __restrict__ y, int32_t* __restrict__ gs) {
     using U = typename UnitOf<TYPE>::T;
     constexpr int UB = units_per_lane<TYPE, B>();
+    constexpr int kStep = 64 * UB;  // units per pass
     const int lane = threadIdx.x & 63;
     const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RW;
-    if (r0 >= M) return;  // the whole wave leaves; nothing below synchronizes across waves
+    const bool wave_ok = r0 < M;
     const int units = K / U::kElems;
     const int glen = units * U::kGroups;  // int32 sums per row and column
+    const uint8_t* wr[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) wr[r] = w + size_t(min(wave_ok ? r0 + r : 0, M - 1)) * nb01;
+    auto unit_of = [&](int kc, int i) {
+        const int u = kc + lane + 64 * i;
+        return u < units ? u : 0;  // units past the row end: a valid unit whose result is dropped
+    };
+    auto load_w = [&](U (&wu)[RW][UB], int kc) {
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+#pragma unroll
+            for (int i = 0; i < UB; ++i) wu[r][i].load(wr[r], unit_of(kc, i));
+    };
     float acc[RW][B];
 #pragma unroll
     for (int r = 0; r < RW; ++r)
 #pragma unroll
         for (int c = 0; c < B; ++c) acc[r][c] = 0.0f;
-
-    for (int kc = 0; kc < units; kc += 64 * UB) {
-        int uu[UB];
-        bool uok[UB];
+    auto compute = [&](const U (&wu)[RW][UB], int kc) {
         ActBlock x[UB][B][U::kActBlocks];
 #pragma unroll
-        for (int i = 0; i < UB; ++i) {
-            const int u = kc + lane + 64 * i;
-            uok[i] = u < units;
-            uu[i] = uok[i] ? u : 0;
+        for (int i = 0; i < UB; ++i)
 #pragma unroll
             for (int c = 0; c < B; ++c)
 #pragma unroll
-                for (int ab = 0; ab < U::kActBlocks; ++ab)
-                    x[i][c][ab] = load_act(xq, xds, K, c, uu[i] * U::kActBlocks + ab);
-        }
-        U wu[RW][UB];
-#pragma unroll
-        for (int r = 0; r < RW; ++r) {
-            const int row = min(r0 + r, M - 1);
-            const uint8_t* wr = w + size_t(row) * nb01;
-#pragma unroll
-            for (int i = 0; i < UB; ++i) wu[r][i].load(wr, uu[i]);
-        }
+                for (int ab = 0; ab < U::kActBlocks; ++ab) x[i][c][ab] = act.get(c, unit_of(kc, i) * U::kActBlocks + ab);
 #pragma unroll
         for (int r = 0; r < RW; ++r) {
             const bool rok = r0 + r < M;
 #pragma unroll
             for (int i = 0; i < UB; ++i) {
+                const int u = kc + lane + 64 * i;
+                const bool uok = u < units;
 #pragma unroll
                 for (int c = 0; c < B; ++c) {
                     int32_t g[U::kGroups];
                     const float v = wu[r][i].acc(x[i][c], acc[r][c], g);
-                    acc[r][c] = uok[i] ? v : acc[r][c];
-                    if (SUMS && uok[i] && rok) {
-                        int32_t* dst = gs + (size_t(c) * M + r0 + r) * glen + size_t(uu[i]) * U::kGroups;
+                    acc[r][c] = uok ? v : acc[r][c];
+                    if (SUMS && uok && rok) {
+                        int32_t* dst = gs + (size_t(c) * M + r0 + r) * glen + size_t(u) * U::kGroups;
 #pragma unroll
                         for (int k = 0; k < U::kGroups; ++k) dst[k] = g[k];
                     }
                 }
             }
         }
+    };
+
+    prep();
+    if (!wave_ok) return;  // the whole wave leaves; nothing below synchronizes across waves
+    const int npass = (units + kStep - 1) / kStep;
+    U w0[RW][UB], w1[RW][UB];
+    load_w(w0, 0);
+    int p = 0;
+    for (; p + 2 < npass; p += 2) {
+        load_w(w1, (p + 1) * kStep);
+        compute(w0, p * kStep);
+        load_w(w0, (p + 2) * kStep);
+        compute(w1, (p + 1) * kStep);
+    }
+    if (p + 1 < npass) {
+        load_w(w1, (p + 1) * kStep);
+        compute(w0, p * kStep);
+        compute(w1, (p + 1) * kStep);
+    } else {
+        compute(w0, p * kStep);
     }
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
@@ -284,18 +400,80 @@ __global__ __launch_bounds__(256) void k_mmvq(const uint8_t* __restrict__ w, int
     }
 }
 
+// LDS layout of a B-column activation: three arrays of B * K/32 16-byte entries.
+struct LdsAct {
+    uint4 *lo, *hi;
+    float4* ds;
+    __device__ LdsAct(uint4* base, int B, int nblk)
+        : lo(base), hi(base + B * nblk), ds(reinterpret_cast<float4*>(base + 2 * B * nblk)) {}
+};
+
+// Activation prepared by p1x_quantize_q8_1: staged into LDS once per work-group when it fits (LDS = true),
+// otherwise read from global memory by every wave.
+template <int TYPE, int B, int RW, bool SUMS, bool LDS>
+__global__ __launch_bounds__(256) void k_mmvq(const uint8_t* __restrict__ w, int64_t nb01, int M, int K,
+                                              const int8_t* __restrict__ xq, const float4* __restrict__ xds,
+                                              float* __restrict__ y, int32_t* __restrict__ gs) {
+    if constexpr (LDS) {
+        extern __shared__ uint4 act_lds[];
+        const int nblk = K / 32;
+        const LdsAct l(act_lds, B, nblk);
+        mmvq_rows<TYPE, B, RW, SUMS>(
+            ActLds{l.lo, l.hi, l.ds, nblk},
+            [&] {
+                copy_to_lds<B>(xq, xds, K, l.lo, l.hi, l.ds);
+                __syncthreads();
+            },
+            w, nb01, M, K, y, gs);
+    } else {
+        mmvq_rows<TYPE, B, RW, SUMS>(ActGlobal{xq, xds, K}, [] {}, w, nb01, M, K, y, gs);
+    }
+}
+
+// The whole op in one launch: the work-group quantizes x into LDS (48 bytes per block and column) before the
+// row loop.
+template <int TYPE, int B, int RW, bool SUMS>
+__global__ __launch_bounds__(256) void k_mmvq_fx(const uint8_t* __restrict__ w, int64_t nb01, int M, int K,
+                                                 const float* __restrict__ x, float* __restrict__ y,
+                                                 int32_t* __restrict__ gs) {
+    extern __shared__ uint4 act_lds[];
+    const int nblk = K / 32;
+    const LdsAct l(act_lds, B, nblk);
+    mmvq_rows<TYPE, B, RW, SUMS>(
+        ActLds{l.lo, l.hi, l.ds, nblk},
+        [&] {
+            quantize_to_lds<B>(x, K, l.lo, l.hi, l.ds);
+            __syncthreads();
+        },
+        w, nb01, M, K, y, gs);
+}
+
 template <int TYPE, int B>
 hipError_t launch_b(const uint8_t* w, int64_t nb01, int M, int K, int rw, const int8_t* xq, const float4* xds,
-                    float* y, int32_t* gs, hipStream_t stream) {
+                    const float* x, float* y, int32_t* gs, hipStream_t stream) {
     if (gs) rw = 1;  // the group-sum export is a check path: one row per wave
     const dim3 grid((M + 4 * rw - 1) / (4 * rw));
-#define P1X_RW(R)                                                                                                \
-    if (rw == R) {                                                                                               \
-        if (gs) hipLaunchKernelGGL((k_mmvq<TYPE, B, R, true>), grid, dim3(256), 0, stream, w, nb01, M, K, xq, xds, \
-                                   y, gs);                                                                       \
-        else hipLaunchKernelGGL((k_mmvq<TYPE, B, R, false>), grid, dim3(256), 0, stream, w, nb01, M, K, xq, xds, \
-                                y, gs);                                                                          \
-        return hipGetLastError();                                                                                \
+    const size_t lds = size_t(48) * B * (K / 32);
+    const bool use_lds = lds <= 65536;
+#define P1X_RW(R)                                                                                                  \
+    if (rw == R) {                                                                                                 \
+        if (x && gs)                                                                                               \
+            hipLaunchKernelGGL((k_mmvq_fx<TYPE, B, R, true>), grid, dim3(256), lds, stream, w, nb01, M, K, x, y, gs); \
+        else if (x)                                                                                                \
+            hipLaunchKernelGGL((k_mmvq_fx<TYPE, B, R, false>), grid, dim3(256), lds, stream, w, nb01, M, K, x, y, gs); \
+        else if (gs && use_lds)                                                                                    \
+            hipLaunchKernelGGL((k_mmvq<TYPE, B, R, true, true>), grid, dim3(256), lds, stream, w, nb01, M, K, xq, xds, y, \
+                               gs);                                                                                \
+        else if (gs)                                                                                               \
+            hipLaunchKernelGGL((k_mmvq<TYPE, B, R, true, false>), grid, dim3(256), 0, stream, w, nb01, M, K, xq, xds, y, \
+                               gs);                                                                                \
+        else if (use_lds)                                                                                          \
+            hipLaunchKernelGGL((k_mmvq<TYPE, B, R, false, true>), grid, dim3(256), lds, stream, w, nb01, M, K, xq, xds, \
+                               y, gs);                                                                             \
+        else                                                                                                       \
+            hipLaunchKernelGGL((k_mmvq<TYPE, B, R, false, false>), grid, dim3(256), 0, stream, w, nb01, M, K, xq, xds, \
+                               y, gs);                                                                             \
+        return hipGetLastError();                                                                                  \
     }
     P1X_RW(1)
     P1X_RW(2)
@@ -306,16 +484,16 @@ hipError_t launch_b(const uint8_t* w, int64_t nb01, int M, int K, int rw, const 
 
 template <int TYPE>
 hipError_t launch_type(int B, const uint8_t* w, int64_t nb01, int M, int K, int rw, const int8_t* xq,
-                       const float4* xds, float* y, int32_t* gs, hipStream_t stream) {
+                       const float4* xds, const float* x, float* y, int32_t* gs, hipStream_t stream) {
     switch (B) {
-        case 1: return launch_b<TYPE, 1>(w, nb01, M, K, rw, xq, xds, y, gs, stream);
-        case 2: return launch_b<TYPE, 2>(w, nb01, M, K, rw, xq, xds, y, gs, stream);
-        case 3: return launch_b<TYPE, 3>(w, nb01, M, K, rw, xq, xds, y, gs, stream);
-        case 4: return launch_b<TYPE, 4>(w, nb01, M, K, rw, xq, xds, y, gs, stream);
-        case 5: return launch_b<TYPE, 5>(w, nb01, M, K, rw, xq, xds, y, gs, stream);
-        case 6: return launch_b<TYPE, 6>(w, nb01, M, K, rw, xq, xds, y, gs, stream);
-        case 7: return launch_b<TYPE, 7>(w, nb01, M, K, rw, xq, xds, y, gs, stream);
-        case 8: return launch_b<TYPE, 8>(w, nb01, M, K, rw, xq, xds, y, gs, stream);
+        case 1: return launch_b<TYPE, 1>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream);
+        case 2: return launch_b<TYPE, 2>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream);
+        case 3: return launch_b<TYPE, 3>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream);
+        case 4: return launch_b<TYPE, 4>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream);
+        case 5: return launch_b<TYPE, 5>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream);
+        case 6: return launch_b<TYPE, 6>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream);
+        case 7: return launch_b<TYPE, 7>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream);
+        case 8: return launch_b<TYPE, 8>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream);
     }
     return hipErrorInvalidValue;
 }
@@ -329,16 +507,25 @@ int mmvq_rows_per_wave(int M) {
     return 1;
 }
 
+// The single-launch form (x quantized into LDS by each work-group) when its 48 bytes per block and column fit in
+// 64 KiB of LDS and the repeated quantization (work-groups x B x K elements) stays small next to the weight
+// stream; otherwise the activation goes through p1x_quantize_q8_1 and a workspace.
+bool mmvq_fused_fits(int B, int M, int K) {
+    const int rw = mmvq_rows_per_wave(M);
+    const long wgs = (M + 4L * rw - 1) / (4L * rw);  // every work-group quantizes all B x K elements
+    return size_t(48) * B * (K / 32) <= 65536 && wgs * K * B <= (1L << 22);
+}
+
 hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
-                       float* y, int32_t* gs, hipStream_t stream) {
+                       const float* x, float* y, int32_t* gs, hipStream_t stream) {
     const int rw = mmvq_rows_per_wave(M);
     const auto* wb = static_cast<const uint8_t*>(w);
     const auto* d4 = reinterpret_cast<const float4*>(xds);
     switch (type) {
-        case Q4_0: return launch_type<Q4_0>(B, wb, nb01, M, K, rw, xq, d4, y, gs, stream);
-        case Q8_0: return launch_type<Q8_0>(B, wb, nb01, M, K, rw, xq, d4, y, gs, stream);
-        case Q4_K: return launch_type<Q4_K>(B, wb, nb01, M, K, rw, xq, d4, y, gs, stream);
-        case Q6_K: return launch_type<Q6_K>(B, wb, nb01, M, K, rw, xq, d4, y, gs, stream);
+        case Q4_0: return launch_type<Q4_0>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
+        case Q8_0: return launch_type<Q8_0>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
+        case Q4_K: return launch_type<Q4_K>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
+        case Q6_K: return launch_type<Q6_K>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
     }
     return hipErrorInvalidValue;
 }
