@@ -24,9 +24,23 @@ typedef uint32_t u32x4v __attribute__((ext_vector_type(4), aligned(4)));
 typedef __attribute__((address_space(1))) const u32x4v gu32x4;
 __device__ __forceinline__ const gu32* global_dwords(uintptr_t a) { return (const gu32*)a; }
 __device__ __forceinline__ const gu32* global_dwords(const void* p) { return global_dwords(reinterpret_cast<uintptr_t>(p)); }
+#ifndef P1X_WEIGHT_NT
+#define P1X_WEIGHT_NT 0  // non-temporal weight loads: measured slower than plain loads in the mat-vec row loop
+#endif
 __device__ __forceinline__ U32x4 ld_u32x4(const gu32* p) {
+#if P1X_WEIGHT_NT
+    const u32x4v v = __builtin_nontemporal_load((const gu32x4*)p);
+#else
     const u32x4v v = *(const gu32x4*)p;
+#endif
     return U32x4{v.x, v.y, v.z, v.w};
+}
+__device__ __forceinline__ uint32_t ld_u32(const gu32* p) {
+#if P1X_WEIGHT_NT
+    return __builtin_nontemporal_load(p);
+#else
+    return *p;
+#endif
 }
 
 // Packed signed int8 dot product with int32 accumulate: v_dot4_i32_i8 (exact).
@@ -49,7 +63,7 @@ __device__ __forceinline__ void load_q4_0_block(const uint8_t* p, uint32_t q[4],
     const gu32* base = global_dwords(addr & ~uintptr_t(3));
     const uint32_t sh = uint32_t(addr & 2);
     const U32x4 v = ld_u32x4(base);
-    const uint32_t w4 = base[4];
+    const uint32_t w4 = ld_u32(base + 4);
     const uint32_t sel = slice_sel(sh);
     q[0] = perm(v.y, v.x, sel);
     q[1] = perm(v.z, v.y, sel);
@@ -62,7 +76,7 @@ __device__ __forceinline__ void load_q8_0_block(const uint8_t* p, uint32_t q[8],
     const gu32* base = global_dwords(addr & ~uintptr_t(3));
     const uint32_t sh = uint32_t(addr & 2);
     const U32x4 v0 = ld_u32x4(base), v1 = ld_u32x4(base + 4);
-    const uint32_t w[9] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w, base[8]};
+    const uint32_t w[9] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w, ld_u32(base + 8)};
     const uint32_t sel = slice_sel(sh);
 #pragma unroll
     for (int j = 0; j < 8; ++j) q[j] = perm(w[j + 1], w[j], sel);
@@ -84,7 +98,7 @@ __device__ __forceinline__ void load_field(const uint8_t* p, uint32_t* out) {
         w[i + 2] = v.z;
         w[i + 3] = v.w;
     }
-    w[N] = base[N];
+    w[N] = ld_u32(base + N);
     const uint32_t sel = (a & 2) ? 0x05040302u : 0x03020100u;  // the field starts at byte 2 or 0 of w[0]
 #pragma unroll
     for (int i = 0; i < N; ++i) out[i] = perm(w[i + 1], w[i], sel);
@@ -93,7 +107,7 @@ __device__ __forceinline__ void load_field(const uint8_t* p, uint32_t* out) {
 // The 16 bits at a 2-byte aligned address (a scale inside a block).
 __device__ __forceinline__ uint32_t load_u16(const uint8_t* p) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    return (*global_dwords(a & ~uintptr_t(3)) >> (8 * (a & 2))) & 0xffffu;
+    return (ld_u32(global_dwords(a & ~uintptr_t(3))) >> (8 * (a & 2))) & 0xffffu;
 }
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {

@@ -16,6 +16,22 @@
 #include "common.h"
 #include "launch.h"
 
+#ifndef P1X_MMVQ_UB
+#define P1X_MMVQ_UB 1  // q4_0 / q8_0 units per lane per pass at ne11 <= 2
+#endif
+#ifndef P1X_MMVQ_MIN_WAVES
+#define P1X_MMVQ_MIN_WAVES 4096  // rows per wave grow while at least this many waves remain
+#endif
+#ifndef P1X_MMVQ_MIN_WAVES_FX
+#define P1X_MMVQ_MIN_WAVES_FX 2048  // the same for the single-launch form (fewer work-groups: less requantizing)
+#endif
+#ifndef P1X_MMVQ_FUSE_MAX
+#define P1X_MMVQ_FUSE_MAX (1L << 21)  // single launch while work-groups x B x K stays at or below this
+#endif
+#ifndef P1X_MMVQ_MAX_RW
+#define P1X_MMVQ_MAX_RW 4
+#endif
+
 namespace p1x {
 namespace {
 
@@ -135,7 +151,7 @@ struct UnitQ4_0 {
         const gu32* base = global_dwords(a & ~uintptr_t(3));
         const U32x4 v = ld_u32x4(base);  // reads only dwords holding block bytes (see common.h)
         w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
-        w[4] = base[4];
+        w[4] = ld_u32(base + 4);
         sh = uint32_t(a & 2);
     }
     __device__ __forceinline__ float acc(const ActBlock* x, float a, int32_t* g) const {
@@ -164,7 +180,7 @@ struct UnitQ8_0 {
         const U32x4 v0 = ld_u32x4(base), v1 = ld_u32x4(base + 4);
         w[0] = v0.x; w[1] = v0.y; w[2] = v0.z; w[3] = v0.w;
         w[4] = v1.x; w[5] = v1.y; w[6] = v1.z; w[7] = v1.w;
-        w[8] = base[8];
+        w[8] = ld_u32(base + 8);
         sh = uint32_t(a & 2);
     }
     __device__ __forceinline__ float acc(const ActBlock* x, float a, int32_t* g) const {
@@ -274,7 +290,7 @@ template <> struct UnitOf<Q6_K> { using T = UnitQ6_K; };
 template <int TYPE, int B>
 constexpr int units_per_lane() {
     if (TYPE == Q4_K || TYPE == Q6_K) return 1;
-    return B <= 2 ? 2 : 1;
+    return B <= 2 ? P1X_MMVQ_UB : 1;
 }
 
 // ------------------------------------------------------------------------------------------------ reduction
@@ -500,10 +516,12 @@ hipError_t launch_type(int B, const uint8_t* w, int64_t nb01, int M, int K, int 
 
 }  // namespace
 
-// Rows per wave: the most (up to 4) that still leaves >= 2048 waves (8 per CU) to fill the 256 CUs.
-int mmvq_rows_per_wave(int M) {
+// Rows per wave: the most (up to 4) that still leaves enough waves to fill the 256 CUs (4096 for the kernel on a
+// prepared activation, 2048 for the single-launch form, which requantizes x once per work-group).
+int mmvq_rows_per_wave(int M, bool fused) {
+    const int min_waves = fused ? P1X_MMVQ_MIN_WAVES_FX : P1X_MMVQ_MIN_WAVES;
     for (int rw : {4, 2})
-        if (M / rw >= 2048) return rw;
+        if (rw <= P1X_MMVQ_MAX_RW && M / rw >= min_waves) return rw;
     return 1;
 }
 
@@ -511,14 +529,14 @@ int mmvq_rows_per_wave(int M) {
 // 64 KiB of LDS and the repeated quantization (work-groups x B x K elements) stays small next to the weight
 // stream; otherwise the activation goes through p1x_quantize_q8_1 and a workspace.
 bool mmvq_fused_fits(int B, int M, int K) {
-    const int rw = mmvq_rows_per_wave(M);
+    const int rw = mmvq_rows_per_wave(M, true);
     const long wgs = (M + 4L * rw - 1) / (4L * rw);  // every work-group quantizes all B x K elements
-    return size_t(48) * B * (K / 32) <= 65536 && wgs * K * B <= (1L << 22);
+    return size_t(48) * B * (K / 32) <= 65536 && wgs * K * B <= P1X_MMVQ_FUSE_MAX;
 }
 
 hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
                        const float* x, float* y, int32_t* gs, hipStream_t stream) {
-    const int rw = mmvq_rows_per_wave(M);
+    const int rw = mmvq_rows_per_wave(M, x != nullptr);
     const auto* wb = static_cast<const uint8_t*>(w);
     const auto* d4 = reinterpret_cast<const float4*>(xds);
     switch (type) {
