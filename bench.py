@@ -215,9 +215,19 @@ def measure_roofline(torch, P, lib, timer, layers, x):
     b = matvec_bytes(P.Q4_0, 4096, 14336, 1)
     achieved = b / (med * 1e-6) / 1e9
     log(f"[bench] Q4_0 4096x14336 mat-vec kernel {med:.2f} us (min {mn:.2f}) -> {achieved:.0f} GB/s")
+    # HBM bytes per launch of this kernel from the FETCH_SIZE / WRITE_SIZE profiler passes (calibrated against a
+    # 32 MiB copy), recorded next to the rocprof summary; null when that record is absent.
+    traffic, src = None, None
+    rec = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    if os.path.exists(rec):
+        with open(rec) as f:
+            t = json.load(f).get("k_mmvq q4_0 4096x14336 ne11=1")
+        if t:
+            traffic, src = t["traffic_bytes"], t["source"]
     return {"kernel": "k_mmvq<q4_0> 4096x14336 (prepared Q8_1 activation)", "bound": "hbm",
             "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4),
-            "traffic": None, "algorithmic_bytes": b, "avg_us": round(med, 3), "min_us": round(mn, 3)}
+            "traffic": traffic, "traffic_unit": "bytes per launch", "traffic_source": src,
+            "algorithmic_bytes": b, "avg_us": round(med, 3), "min_us": round(mn, 3)}
 
 
 def measure_fa(torch, P, lib, timer, gen, ctxs):
