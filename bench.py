@@ -87,9 +87,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline and roofline only")
-    ap.add_argument("--only", choices=("roofline", "fa"), default=None,
-                    help="run one kernel measurement alone (for profiler runs whose per-kernel averages must not "
-                         "mix shapes): 'roofline' = the Q4_0 4096x14336 mat-vec, 'fa' = FA decode at --fa-ctx")
+    ap.add_argument("--only", choices=("roofline", "fa", "decode"), default=None,
+                    help="run one measurement alone (for profiler runs whose per-kernel averages must not mix "
+                         "shapes): 'roofline' = the Q4_0 4096x14336 mat-vec, 'fa' = FA decode at --fa-ctx, "
+                         "'decode' = the end-to-end 8B greedy decode")
     ap.add_argument("--fa-ctx", type=int, nargs="+", default=[512, 640, 2048, 8192, 32768])
     args = ap.parse_args()
     if args.gpus != 1:
@@ -104,6 +105,9 @@ def main():
 
     lib = P.load()
     dev = torch.device("cuda")
+    if args.only == "decode":
+        print(json.dumps({"only": "decode", "decode_8b": measure_decode(torch)}))
+        return
     log(f"[bench] {torch.cuda.get_device_name(0)}; building {args.layers} Q4_0 layers")
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1234)
@@ -189,7 +193,8 @@ def main():
         "config": {"workload": "Llama-3-8B layer mat-vec sweep, Q4_0, ne11=1: Wq 4096x4096, Wk/Wv 1024x4096, "
                                "Wo 4096x4096, gate/up 14336x4096, down 4096x14336; weights N(0,0.02) quantized "
                                "with ggml's q4_0 reference rule, x N(0,1); 8 weight sets rotated (982 MB)",
-                   "op": "quantize_q8_1 + mul_mat_vec per matrix (14 launches per step)", "launch": "hip-graph",
+                   "op": "p1x_mul_mat_vec per matrix: one launch with in-kernel Q8_1 for Wq/Wk/Wv/Wo, Q8_1 "
+                         "quantize + mat-vec for gate/up/down (10 launches per step)", "launch": "hip-graph",
                    "bytes_per_step": step_bytes, "pct_hbm_peak": round(100 * value / PEAK_GBS, 2)},
         "roofline": roof,
     }
@@ -342,6 +347,56 @@ def extra_measurements(torch, P, lib, synth, timer, gen, layers, xs, ctxs):
         "note": "sum of measured graph periods: 32 x (layer step with shared Q8_1 + FA decode @ctx 640) + Q4_0 "
                 "128256x4096 output projection; excludes norm/RoPE/SwiGLU/KV-append glue kernels"}
     log(f"[bench] 8B decode kernel-sum estimate {1e6 / token_us:.1f} tok/s")
+    del wout
+    out["decode_8b"] = measure_decode(torch)
+    return out
+
+
+def measure_decode(torch, n_prompt=512, n_gen=256, seed=7):
+    """End-to-end greedy decode of the random-init Llama-3-8B-shaped Q4_0 model (32 layers, fp16 KV cache):
+    the prompt's positions then n_gen decode steps, each step one replay of a captured p1x_llama_decode_step
+    graph (a whole token: embedding, 32 layers, output projection, argmax); decode tok/s = n_gen / time."""
+    from p100_amd import llama
+
+    hp = llama.hparams(n_prompt + n_gen)
+    t_build = time.time()
+    model = llama.LlamaModel(hp, device="cuda", seed=seed)
+    torch.cuda.synchronize()
+    t_build = time.time() - t_build
+    dec = llama.Decoder(model, max_prompt=n_prompt)
+    g = torch.Generator().manual_seed(seed)
+    prompt = torch.randint(0, hp.n_vocab, (n_prompt,), generator=g).tolist()
+    dec.reset(prompt)
+    dec.capture()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    ev[0].record()
+    dec.run(n_prompt)
+    ev[1].record()
+    dec.run(n_gen)
+    ev[2].record()
+    torch.cuda.synchronize()
+    prompt_ms, gen_ms = ev[0].elapsed_time(ev[1]), ev[1].elapsed_time(ev[2])
+    state = dec.state.tolist()
+    toks = dec.tokens[n_prompt:n_prompt + n_gen + 1].tolist()
+    if state[0] != n_prompt + n_gen or not all(0 <= t < hp.n_vocab for t in toks):
+        raise RuntimeError(f"decode ended in an unexpected state {state[:3]}")
+    kv_read = sum(fa_bytes(hp.n_head, hp.n_head_kv, p + 1, hp.head_dim) for p in range(n_prompt, n_prompt + n_gen))
+    token_bytes = model.weight_bytes() + kv_read / n_gen
+    us_tok = gen_ms * 1e3 / n_gen
+    out = {
+        "tok_s": round(n_gen / (gen_ms * 1e-3), 1), "us_per_token": round(us_tok, 1),
+        "gbs": round(token_bytes / (us_tok * 1e-6) / 1e9, 1),
+        "roofline_tok_s": round(PEAK_GBS * 1e9 / token_bytes, 1), "bytes_per_token": int(token_bytes),
+        "prompt_positions_tok_s": round(n_prompt / (prompt_ms * 1e-3), 1),
+        "config": f"Llama-3-8B shape (32 layers, 4096, FFN 14336, 32/8 heads x 128, vocab 128256), Q4_0 weights "
+                  f"N(0,0.02) random-init, fp16 KV cache; prompt {n_prompt} random ids fed through the decode step, "
+                  f"then {n_gen} greedy decode steps timed; one HIP graph per token replayed",
+        "launches_per_token": 2 + hp.n_layer * 10 + 3, "weights_build_s": round(t_build, 1),
+    }
+    log(f"[bench] 8B decode: {out['tok_s']} tok/s ({us_tok:.1f} us/token, {out['gbs']} GB/s), "
+        f"prompt positions {out['prompt_positions_tok_s']} tok/s")
+    del dec, model
+    torch.cuda.empty_cache()
     return out
 
 

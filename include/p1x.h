@@ -26,6 +26,17 @@
  *   p1x_flash_attn_decode    ggml_cuda_flash_attn_ext for n_q small with f16 K/V (fattn.cu:541-719 selection;
  *                            flash_attn_tile + flash_attn_combine_results, 0004 patch); CPU contract
  *                            p100::attention_reference (include/p100/attention.h:48-49)
+ *   p1x_flash_attn_decode_kvlen  the same op over a KV-cache view whose valid length is known only on the device
+ *                            (llama.cpp pads the view and masks the tail with the KQ mask; here the length is read)
+ * Decode-step glue and driver (the llama-bench decode runs, bench/phase0.sh:124, of the 8B shape modelled in
+ * bin/decode-model.py:52-57; the ggml ops are restated from llama.cpp's Llama graph, not from this reference):
+ *   p1x_get_rows             GGML_OP_GET_ROWS (token embedding), q4_0 / q8_0 rows
+ *   p1x_rms_norm_q8_1        GGML_OP_ADD (residual) + GGML_OP_RMS_NORM + GGML_OP_MUL, emitting the Q8_1
+ *                            activation of the next GGML_OP_MUL_MAT
+ *   p1x_swiglu_q8_1          GGML_OP_GLU (swiglu), emitting the Q8_1 activation of the down projection
+ *   p1x_rope_kv_append       GGML_OP_ROPE (normal mode) of q and k + GGML_OP_SET_ROWS of k and v into the cache
+ *   p1x_argmax               GGML_OP_ARGMAX (greedy sampling)
+ *   p1x_llama_decode_step    one token of llm_build_llama at batch 1 over all of the above
  */
 #ifndef P1X_H
 #define P1X_H
@@ -122,8 +133,100 @@ int p1x_flash_attn_decode(const p1x_attn_params* p, const float* q, const uint16
                           const p1x_kv_strides* strides, const float* mask, float* o, float* lse, void* ws,
                           size_t ws_bytes, void* stream);
 
+/*
+ * p1x_flash_attn_decode over a KV cache of capacity p->seq_kv rows of which only *kv_len (device int32, read when
+ * the kernels run; clamped to [0, seq_kv]) are valid: the split plan and the workspace are those of seq_kv, the
+ * keys are rows [0, *kv_len), and the causal alignment (when p->causal) is to *kv_len. One recorded launch
+ * (e.g. in a HIP graph) then serves every length up to the capacity. mask rows keep the stride seq_kv.
+ */
+int p1x_flash_attn_decode_kvlen(const p1x_attn_params* p, const float* q, const uint16_t* k, const uint16_t* v,
+                                const p1x_kv_strides* strides, const float* mask, const int32_t* kv_len, float* o,
+                                float* lse, void* ws, size_t ws_bytes, void* stream);
+
 /* fp32 -> IEEE binary16 bits with the device conversion the kernels use (round to nearest even). */
 int p1x_round_to_fp16(const float* x, uint16_t* out, int64_t n, void* stream);
+
+/* ------------------------------------------------------------------------------------ decode-step glue */
+
+/* out[i] = dequantized element i of row *row (device int32) of a q4_0 or q8_0 matrix of n_rows rows, i < K
+ * (ggml's dequantize_q4_0: d * (q - 8); dequantize_q8_0: d * q). A row index outside [0, n_rows) reads row 0. */
+int p1x_get_rows(int wtype, const void* w, int64_t nb01, int64_t n_rows, int64_t K, const int32_t* row, float* out,
+                 void* stream);
+
+/* x[i] += add[i] when add is not NULL (x, the residual stream, is updated in place); then
+ * h = (x * rsqrt(mean(x^2) + eps)) * w and its Q8_1 activation (qs, ds as p1x_quantize_q8_1, one column).
+ * h_out (f32 [n]) optional. n % 32 == 0, n <= 16384. */
+int p1x_rms_norm_q8_1(float* x, const float* add, const float* w, int64_t n, float eps, int8_t* qs, float* ds,
+                      float* h_out, void* stream);
+
+/* h = silu(gate) * up with silu(g) = g / (1 + exp(-g)), and its Q8_1 activation; h_out optional. n % 32 == 0. */
+int p1x_swiglu_q8_1(const float* gate, const float* up, int64_t n, int8_t* qs, float* ds, float* h_out, void* stream);
+
+/* Rotary embedding, llama.cpp's normal mode: pair p = (x[2p], x[2p+1]) of each head rotates by
+ * theta = pos * rope_base^(-2p/head_dim). q [n_head][head_dim] -> q_out; k [n_head_kv][head_dim] -> fp16 row pos
+ * of k_cache; v -> fp16 row pos of v_cache. Caches are fp16 [n_head_kv][n_ctx][head_dim]; pos is a device int32
+ * read when the kernel runs; a position outside [0, n_ctx) writes no cache row. head_dim even. */
+int p1x_rope_kv_append(const float* q, const float* k, const float* v, float* q_out, uint16_t* k_cache,
+                       uint16_t* v_cache, int n_head, int n_head_kv, int head_dim, int n_ctx, const int32_t* pos,
+                       float rope_base, void* stream);
+
+/* *out = index of the largest x[i] (the first on ties; NaN never wins; -1 when every value is NaN). */
+size_t p1x_argmax_workspace(int64_t n);
+int p1x_argmax(const float* x, int64_t n, int32_t* out, void* ws, size_t ws_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------ Llama decode step */
+
+typedef struct {
+    int n_layer, n_embd, n_head, n_head_kv, n_ff, n_vocab;
+    int n_ctx;        /* KV-cache capacity in positions */
+    int wtype;        /* type of the layer matrices (q4_0, q8_0, q4_K, q6_K) */
+    int embd_type;    /* token embedding type (q4_0 or q8_0) */
+    int output_type;  /* output projection type (any of the four) */
+    float rms_eps;    /* 1e-5 for Llama 3 */
+    float rope_base;  /* 500000 for Llama 3 */
+} p1x_llama_hparams;
+
+/* One layer: GGUF matrices with dense rows (row stride K / block * block bytes), f32 norm weights, fp16 caches
+ * [n_head_kv][n_ctx][head_dim]. When wk follows wq and wv follows wk in memory (and w_up follows w_gate), the
+ * step runs each group as one mat-vec launch. */
+typedef struct {
+    const float* attn_norm;
+    const void *wq, *wk, *wv, *wo;
+    const float* ffn_norm;
+    const void *w_gate, *w_up, *w_down;
+    uint16_t *k_cache, *v_cache;
+} p1x_llama_layer;
+
+typedef struct {
+    p1x_llama_hparams hp;
+    const void* tok_embd;           /* n_vocab rows of embd_type over n_embd */
+    const p1x_llama_layer* layers;  /* host array of n_layer */
+    const float* output_norm;
+    const void* output;             /* n_vocab rows of output_type over n_embd */
+} p1x_llama_model;
+
+/* Device-resident state of a greedy decode (device memory, int32 each). */
+typedef struct {
+    int32_t pos;       /* position decoded by the next step */
+    int32_t n_prompt;  /* prompt[0 .. n_prompt) feeds positions [0, n_prompt) */
+    int32_t n_kv;      /* visible KV length of the current step (written by the step) */
+    int32_t reserved;
+} p1x_decode_state;
+
+size_t p1x_llama_workspace(const p1x_llama_hparams* hp);
+
+/*
+ * One decode step of a Llama-architecture model at batch 1, entirely on `stream`, reading its position from
+ * *state (device memory) when it runs: token t = prompt[pos] if pos < n_prompt else tokens[pos]; embedding; per
+ * layer RMSNorm, q/k/v, RoPE + KV append at row pos, attention over rows [0, pos], o projection, residual,
+ * RMSNorm, gate/up, SwiGLU, down, residual; final RMSNorm, output projection into logits (f32 [n_vocab], or the
+ * workspace when NULL), greedy argmax into tokens[pos + 1], and pos += 1. Because nothing position-dependent is
+ * baked into the launches, the step can be captured once into a HIP graph and replayed for every position.
+ * tokens: device int32 [n_ctx + 1]; prompt: device int32 [n_prompt] (n_prompt <= n_ctx). A position outside
+ * [0, n_ctx) writes no cache row and does not advance.
+ */
+int p1x_llama_decode_step(const p1x_llama_model* m, p1x_decode_state* state, const int32_t* prompt, int32_t* tokens,
+                          float* logits, void* ws, size_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

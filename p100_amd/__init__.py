@@ -32,7 +32,9 @@ ACT = {"q8_1": 0, "h16": 1}
 OK, EINVAL, EUNSUPPORTED, EHIP, EWORKSPACE = 0, 1, 2, 3, 4
 EXPORTS = ["p1x_version", "p1x_init", "p1x_last_error", "p1x_quantize_q8_1", "p1x_prepare_h16",
            "p1x_mul_mat_vec_workspace", "p1x_mul_mat_vec", "p1x_mul_mat_vec_q8_1", "p1x_mul_mat_vec_h16",
-           "p1x_attn_validate", "p1x_flash_attn_decode_workspace", "p1x_flash_attn_decode", "p1x_round_to_fp16"]
+           "p1x_attn_validate", "p1x_flash_attn_decode_workspace", "p1x_flash_attn_decode",
+           "p1x_flash_attn_decode_kvlen", "p1x_round_to_fp16", "p1x_get_rows", "p1x_rms_norm_q8_1", "p1x_swiglu_q8_1",
+           "p1x_rope_kv_append", "p1x_argmax_workspace", "p1x_argmax", "p1x_llama_workspace", "p1x_llama_decode_step"]
 
 
 class P1XError(RuntimeError):
@@ -88,7 +90,17 @@ def load():
         "p1x_flash_attn_decode_workspace": (sz, [C.POINTER(AttnParams)]),
         "p1x_flash_attn_decode": (C.c_int, [C.POINTER(AttnParams), vp, vp, vp, C.POINTER(KVStrides), vp, vp, vp,
                                             vp, sz, vp]),
+        "p1x_flash_attn_decode_kvlen": (C.c_int, [C.POINTER(AttnParams), vp, vp, vp, C.POINTER(KVStrides), vp, vp,
+                                                  vp, vp, vp, sz, vp]),
         "p1x_round_to_fp16": (C.c_int, [vp, vp, i64, vp]),
+        "p1x_get_rows": (C.c_int, [C.c_int, vp, i64, i64, i64, vp, vp, vp]),
+        "p1x_rms_norm_q8_1": (C.c_int, [vp, vp, vp, i64, C.c_float, vp, vp, vp, vp]),
+        "p1x_swiglu_q8_1": (C.c_int, [vp, vp, i64, vp, vp, vp, vp]),
+        "p1x_rope_kv_append": (C.c_int, [vp, vp, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, vp, C.c_float, vp]),
+        "p1x_argmax_workspace": (sz, [i64]),
+        "p1x_argmax": (C.c_int, [vp, i64, vp, vp, sz, vp]),
+        "p1x_llama_workspace": (sz, [vp]),
+        "p1x_llama_decode_step": (C.c_int, [vp, vp, vp, vp, vp, vp, sz, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -241,11 +253,13 @@ def flash_attn_decode_workspace(p: AttnParams) -> int:
 
 
 def flash_attn_decode(p: AttnParams, q, k, v, mask=None, strides: KVStrides | None = None, want_lse=True, out=None,
-                      lse=None, workspace=None, stream=None):
+                      lse=None, workspace=None, stream=None, kv_len=None):
     """o, lse = attention(q, k, v) with the contract of p100::attention_reference.
 
     q float32 [batch, n_head_q, seq_q, d]; k, v float16 [batch, n_head_kv, seq_kv, d] (or strided views with
     ``strides``); mask optional float32 [seq_q, seq_kv]. Raises ValueError(reason) for invalid parameters.
+    kv_len: optional device int32 tensor; when given, only its first element's count of K/V rows is valid (read
+    when the kernels run), p.seq_kv being the cache capacity.
     """
     import torch
 
@@ -263,8 +277,13 @@ def flash_attn_decode(p: AttnParams, q, k, v, mask=None, strides: KVStrides | No
     if ws.numel() * ws.element_size() < need:
         raise P1XError(EWORKSPACE, f"workspace of {need} bytes required")
     sp = C.byref(strides) if strides is not None else None
-    _check(lib.p1x_flash_attn_decode(C.byref(p), _ptr(q), _ptr(k), _ptr(v), sp, _ptr(mask), _ptr(o), _ptr(l_out),
-                                     _ptr(ws), ws.numel() * ws.element_size(), _stream(stream)))
+    nbytes = ws.numel() * ws.element_size()
+    if kv_len is None:
+        _check(lib.p1x_flash_attn_decode(C.byref(p), _ptr(q), _ptr(k), _ptr(v), sp, _ptr(mask), _ptr(o), _ptr(l_out),
+                                         _ptr(ws), nbytes, _stream(stream)))
+    else:
+        _check(lib.p1x_flash_attn_decode_kvlen(C.byref(p), _ptr(q), _ptr(k), _ptr(v), sp, _ptr(mask), _ptr(kv_len),
+                                               _ptr(o), _ptr(l_out), _ptr(ws), nbytes, _stream(stream)))
     return o, l_out
 
 
@@ -276,4 +295,69 @@ def round_to_fp16(x, stream=None):
     x = x.contiguous()
     out = torch.empty(x.shape, dtype=torch.int16, device=x.device)
     _check(lib.p1x_round_to_fp16(_ptr(x), _ptr(out), x.numel(), _stream(stream)))
+    return out
+
+
+# ------------------------------------------------------------------------------------------------ decode glue
+def get_rows(wtype, w, n_rows, K, row, nb01=None, out=None, stream=None):
+    """out[K] = dequantized row *row (device int32 tensor) of a q4_0 / q8_0 matrix (ggml GET_ROWS)."""
+    import torch
+
+    lib = load()
+    wtype = TYPES.get(wtype, wtype)
+    nb01 = row_bytes(wtype, K) if nb01 is None else nb01
+    y = out if out is not None else torch.empty(K, dtype=torch.float32, device=w.device)
+    _check(lib.p1x_get_rows(wtype, _ptr(w), nb01, n_rows, K, _ptr(row), _ptr(y), _stream(stream)))
+    return y
+
+
+def rms_norm_q8_1(x, w, eps=1e-5, add=None, want_h=False, stream=None):
+    """x += add (in place, when given); h = x * rsqrt(mean(x^2) + eps) * w; returns Q81(h) (and h)."""
+    import torch
+
+    lib = load()
+    n = x.numel()
+    qs = torch.empty((1, n), dtype=torch.int8, device=x.device)
+    ds = torch.empty((1, n // 32, 4), dtype=torch.float32, device=x.device)
+    h = torch.empty(n, dtype=torch.float32, device=x.device) if want_h else None
+    _check(lib.p1x_rms_norm_q8_1(_ptr(x), _ptr(add), _ptr(w), n, eps, _ptr(qs), _ptr(ds), _ptr(h), _stream(stream)))
+    return (Q81(qs, ds), h) if want_h else Q81(qs, ds)
+
+
+def swiglu_q8_1(gate, up, want_h=False, stream=None):
+    """h = silu(gate) * up; returns Q81(h) (and h)."""
+    import torch
+
+    lib = load()
+    n = gate.numel()
+    qs = torch.empty((1, n), dtype=torch.int8, device=gate.device)
+    ds = torch.empty((1, n // 32, 4), dtype=torch.float32, device=gate.device)
+    h = torch.empty(n, dtype=torch.float32, device=gate.device) if want_h else None
+    _check(lib.p1x_swiglu_q8_1(_ptr(gate), _ptr(up), n, _ptr(qs), _ptr(ds), _ptr(h), _stream(stream)))
+    return (Q81(qs, ds), h) if want_h else Q81(qs, ds)
+
+
+def rope_kv_append(q, k, v, k_cache, v_cache, pos, rope_base=500000.0, q_out=None, stream=None):
+    """RoPE (normal mode) of q [n_head, d] into q_out and of k [n_head_kv, d] into row *pos of k_cache; v into
+    row *pos of v_cache. Caches float16 [n_head_kv, n_ctx, d]; pos a device int32 tensor. Returns q_out."""
+    import torch
+
+    lib = load()
+    n_head, d = q.shape
+    n_head_kv, n_ctx = k_cache.shape[0], k_cache.shape[1]
+    qo = q_out if q_out is not None else torch.empty_like(q)
+    _check(lib.p1x_rope_kv_append(_ptr(q), _ptr(k), _ptr(v), _ptr(qo), _ptr(k_cache), _ptr(v_cache), n_head,
+                                  n_head_kv, d, n_ctx, _ptr(pos), rope_base, _stream(stream)))
+    return qo
+
+
+def argmax(x, stream=None):
+    """Index of the largest element (first on ties; NaN never wins) as a device int32 tensor of one element."""
+    import torch
+
+    lib = load()
+    n = x.numel()
+    ws = torch.empty(max(lib.p1x_argmax_workspace(n), 8), dtype=torch.uint8, device=x.device)
+    out = torch.empty(1, dtype=torch.int32, device=x.device)
+    _check(lib.p1x_argmax(_ptr(x), n, _ptr(out), _ptr(ws), ws.numel(), _stream(stream)))
     return out

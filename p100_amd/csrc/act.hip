@@ -1,30 +1,12 @@
 // Activation preparation kernels: Q8_1 quantization and the h16 (block-scaled FP16) pre-pass.
 //
-// Each 32-element activation block is handled by one half of a wave64 (32 lanes, one element per lane);
-// the block reductions are the xor butterfly over those 32 lanes with offsets 16, 8, 4, 2, 1, the exact
-// FP32 order of the reference (src/reference/qmv_model.cpp:44-52). Since a+b == b+a in IEEE arithmetic,
-// every lane of the half ends with the same, order-defined sum.
+// Each 32-element activation block is handled by one half of a wave64 (32 lanes, one element per lane), with
+// the half-wave butterflies of common.h.
 #include "common.h"
 #include "launch.h"
 
 namespace p1x {
 namespace {
-
-__device__ __forceinline__ float half_max(float v) {
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
-__device__ __forceinline__ float half_sum(float v) {
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
-__device__ __forceinline__ int half_isum(int v) {
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
 
 // Q8_1 (qmv_model.cpp:60-68, quantize.cu:88-110): d = amax/127 (IEEE division), q = round(x/d) with ties
 // away from zero, s = fp16(sum of the original x), plus the exact integer sum of q for k-quant minima.
@@ -34,15 +16,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8_1(const float* __restrict__
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= K) return;
     const size_t col = blockIdx.y;
-    const float v = x[col * K + i];
-    const float amax = half_max(fabsf(v));
-    const float d = amax / 127.0f;
-    const int q = amax == 0.0f ? 0 : static_cast<int>(roundf(v / d));
-    qs[col * K + i] = static_cast<int8_t>(q);
-    const float s = half_sum(v);
-    const int isum = half_isum(q);
-    if ((threadIdx.x & 31) == 0)
-        ds[col * (K / 32) + i / 32] = make_float4(round_fp16(d), round_fp16(s), static_cast<float>(isum), 0.0f);
+    q8_1_store(x[col * K + i], i, qs + col * K, ds + col * (K / 32));
 }
 
 // h16 pre-pass (qmv_model.cpp:57-68; 0005 patch :185-207): s = amax, x^ = fp16(x/s) stored at the permuted
@@ -53,12 +27,12 @@ __global__ __launch_bounds__(256) void k_prepare_h16(const float* __restrict__ x
     if (i >= K) return;
     const size_t col = blockIdx.y;
     const float v = x[col * K + i];
-    const float s = half_max(fabsf(v));
+    const float s = half_max32(fabsf(v));
     const __half hv = __float2half(s == 0.0f ? 0.0f : v / s);
     const int lane = i & 31;
     const int p = (lane & ~3) | ((lane & 1) << 1) | ((lane & 2) >> 1);
     h[col * K + (i - lane) + p] = __half_as_ushort(hv);
-    const float sum = half_sum(__half2float(hv));
+    const float sum = half_sum32(__half2float(hv));
     if (lane == 0) meta[col * (K / 32) + i / 32] = make_float2(s, sum);
 }
 

@@ -9,11 +9,9 @@
 #include <mutex>
 #include <string>
 
-#include "../../include/p1x.h"
+#include "capi_internal.h"
 
-#include "launch.h"
-
-namespace {
+namespace p1x::capi {
 
 thread_local std::string g_error;
 
@@ -25,6 +23,7 @@ int hip_fail(hipError_t e, const char* what) {
     return fail(P1X_EHIP, std::string(what) + ": " + hipGetErrorName(e) + ": " + hipGetErrorString(e));
 }
 
+namespace {
 std::once_flag g_once;
 int g_init_status = P1X_OK;
 std::string g_init_error;
@@ -49,6 +48,7 @@ void init_once() {
         g_init_error = std::string("this library is built for gfx950 only; device 0 is ") + prop.gcnArchName;
     }
 }
+}  // namespace
 
 int ensure_init() {
     std::call_once(g_once, init_once);
@@ -96,7 +96,72 @@ const char* attn_reason(const p1x_attn_params* p) {
     return nullptr;
 }
 
-}  // namespace
+size_t fa_workspace(const p1x_attn_params* p) {
+    if (!p || attn_reason(p)) return 0;
+    int splits = 0, chunk = 0;
+    fa_split_plan(p->batch, p->n_head_q, p->n_head_kv, p->seq_q, p->seq_kv, p->d_qk, splits, chunk);
+    return splits == 1 ? 0 : size_t(p->batch) * p->n_head_q * p->seq_q * splits * (p->d_v + 2) * sizeof(float);
+}
+
+int fa_prepare(const p1x_attn_params* p, const float* q, const uint16_t* k, const uint16_t* v,
+               const p1x_kv_strides* strides, const float* mask, const int32_t* kv_len, float* o, float* lse, void* ws,
+               size_t ws_bytes, FaArgs& a) {
+    if (int rc = p1x_attn_validate(p)) return rc;
+    if (!q || !k || !v || !o) return fail(P1X_EINVAL, "null q, k, v or o pointer");
+    if (p->d_qk != p->d_v || (p->d_qk != 64 && p->d_qk != 128 && p->d_qk != 256))
+        return fail(P1X_EUNSUPPORTED, "decode kernel supports d_qk == d_v in {64, 128, 256}");
+    const int64_t head_chunks = (p->n_head_q / p->n_head_kv) / fa_heads_per_wg(p->n_head_q, p->n_head_kv);
+    if (p->seq_q > 65535 || int64_t(p->batch) * p->n_head_kv * head_chunks > 65535)
+        return fail(P1X_EUNSUPPORTED, "seq_q and batch*n_head_kv*(query heads per KV head / heads per group) must be <= 65535");
+    if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16))
+        return fail(P1X_EINVAL, "q, k and v must be 16-byte aligned");
+    const int64_t d = p->d_qk;
+    a = FaArgs{};
+    a.q = q;
+    a.k = reinterpret_cast<const __half*>(k);
+    a.v = reinterpret_cast<const __half*>(v);
+    a.mask = mask;
+    a.kv_len = kv_len;
+    if (strides) {
+        a.k_row = strides->k_row, a.k_head = strides->k_head, a.k_batch = strides->k_batch;
+        a.v_row = strides->v_row, a.v_head = strides->v_head, a.v_batch = strides->v_batch;
+        if (a.k_row % 8 || a.k_head % 8 || a.k_batch % 8 || a.v_row % 8 || a.v_head % 8 || a.v_batch % 8)
+            return fail(P1X_EINVAL, "K/V element strides must be multiples of 8 (16-byte rows)");
+        if (a.k_row < d || a.v_row < d) return fail(P1X_EINVAL, "K/V row stride shorter than a row");
+    } else {
+        a.k_row = a.v_row = d;
+        a.k_head = a.v_head = d * p->seq_kv;
+        a.k_batch = a.v_batch = d * p->seq_kv * p->n_head_kv;
+    }
+    // Bytes spanned by one head's seq_kv rows (the kernels' buffer range): 32-bit offsets.
+    const int64_t k_span = ((int64_t(p->seq_kv) - 1) * a.k_row + d) * 2, v_span = ((int64_t(p->seq_kv) - 1) * a.v_row + d) * 2;
+    if (k_span > 0x7ffffff0 || v_span > 0x7ffffff0)
+        return fail(P1X_EUNSUPPORTED, "one head's K or V rows must span less than 2 GiB");
+    a.k_bytes = uint32_t(k_span);
+    a.v_bytes = uint32_t(v_span);
+    a.hq = p->n_head_q;
+    a.hkv = p->n_head_kv;
+    a.seq_q = p->seq_q;
+    a.seq_kv = p->seq_kv;
+    a.causal = p->causal != 0;
+    a.scale = p->scale == 0.0f ? 1.0f / std::sqrt(float(p->d_qk)) : p->scale;
+    a.softcap = p->softcap;
+    fa_split_plan(p->batch, p->n_head_q, p->n_head_kv, p->seq_q, p->seq_kv, p->d_qk, a.splits, a.chunk);
+    const size_t need = fa_workspace(p);
+    if (need && (!ws || ws_bytes < need))
+        return fail(P1X_EWORKSPACE, "workspace of " + std::to_string(need) + " bytes required");
+    if (need && !aligned(ws, 16)) return fail(P1X_EINVAL, "workspace must be 16-byte aligned");
+    const size_t n_part = size_t(p->batch) * p->n_head_q * p->seq_q * a.splits;
+    a.part_o = static_cast<float*>(ws);
+    a.part_ml = reinterpret_cast<float2*>(a.part_o + n_part * d);
+    a.o = o;
+    a.lse = lse;
+    return P1X_OK;
+}
+
+}  // namespace p1x::capi
+
+using namespace p1x::capi;
 
 extern "C" {
 
@@ -199,68 +264,28 @@ int p1x_attn_validate(const p1x_attn_params* p) {
 }
 
 // Workspace: the split partials, O [groups][splits][heads][d] then (max, sum) [groups][splits][heads].
-size_t p1x_flash_attn_decode_workspace(const p1x_attn_params* p) {
-    if (!p || attn_reason(p)) return 0;
-    int splits = 0, chunk = 0;
-    p1x::fa_split_plan(p->batch, p->n_head_q, p->n_head_kv, p->seq_q, p->seq_kv, p->d_qk, splits, chunk);
-    return splits == 1 ? 0 : size_t(p->batch) * p->n_head_q * p->seq_q * splits * (p->d_v + 2) * sizeof(float);
-}
+size_t p1x_flash_attn_decode_workspace(const p1x_attn_params* p) { return fa_workspace(p); }
 
 int p1x_flash_attn_decode(const p1x_attn_params* p, const float* q, const uint16_t* k, const uint16_t* v,
                           const p1x_kv_strides* strides, const float* mask, float* o, float* lse, void* ws,
                           size_t ws_bytes, void* stream) {
     if (int rc = ensure_init()) return rc;
-    if (int rc = p1x_attn_validate(p)) return rc;
-    if (!q || !k || !v || !o) return fail(P1X_EINVAL, "null q, k, v or o pointer");
-    if (p->d_qk != p->d_v || (p->d_qk != 64 && p->d_qk != 128 && p->d_qk != 256))
-        return fail(P1X_EUNSUPPORTED, "decode kernel supports d_qk == d_v in {64, 128, 256}");
-    const int64_t head_chunks = (p->n_head_q / p->n_head_kv) / p1x::fa_heads_per_wg(p->n_head_q, p->n_head_kv);
-    if (p->seq_q > 65535 || int64_t(p->batch) * p->n_head_kv * head_chunks > 65535)
-        return fail(P1X_EUNSUPPORTED, "seq_q and batch*n_head_kv*(query heads per KV head / heads per group) must be <= 65535");
-    if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16))
-        return fail(P1X_EINVAL, "q, k and v must be 16-byte aligned");
-    const int64_t d = p->d_qk;
-    p1x::FaArgs a{};
-    a.q = q;
-    a.k = reinterpret_cast<const __half*>(k);
-    a.v = reinterpret_cast<const __half*>(v);
-    a.mask = mask;
-    if (strides) {
-        a.k_row = strides->k_row, a.k_head = strides->k_head, a.k_batch = strides->k_batch;
-        a.v_row = strides->v_row, a.v_head = strides->v_head, a.v_batch = strides->v_batch;
-        if (a.k_row % 8 || a.k_head % 8 || a.k_batch % 8 || a.v_row % 8 || a.v_head % 8 || a.v_batch % 8)
-            return fail(P1X_EINVAL, "K/V element strides must be multiples of 8 (16-byte rows)");
-        if (a.k_row < d || a.v_row < d) return fail(P1X_EINVAL, "K/V row stride shorter than a row");
-    } else {
-        a.k_row = a.v_row = d;
-        a.k_head = a.v_head = d * p->seq_kv;
-        a.k_batch = a.v_batch = d * p->seq_kv * p->n_head_kv;
-    }
-    // Bytes spanned by one head's seq_kv rows (the kernels' buffer range): 32-bit offsets.
-    const int64_t k_span = ((int64_t(p->seq_kv) - 1) * a.k_row + d) * 2, v_span = ((int64_t(p->seq_kv) - 1) * a.v_row + d) * 2;
-    if (k_span > 0x7ffffff0 || v_span > 0x7ffffff0)
-        return fail(P1X_EUNSUPPORTED, "one head's K or V rows must span less than 2 GiB");
-    a.k_bytes = uint32_t(k_span);
-    a.v_bytes = uint32_t(v_span);
-    a.hq = p->n_head_q;
-    a.hkv = p->n_head_kv;
-    a.seq_q = p->seq_q;
-    a.seq_kv = p->seq_kv;
-    a.causal = p->causal != 0;
-    a.scale = p->scale == 0.0f ? 1.0f / std::sqrt(float(p->d_qk)) : p->scale;
-    a.softcap = p->softcap;
-    p1x::fa_split_plan(p->batch, p->n_head_q, p->n_head_kv, p->seq_q, p->seq_kv, p->d_qk, a.splits, a.chunk);
-    const size_t need = p1x_flash_attn_decode_workspace(p);
-    if (need && (!ws || ws_bytes < need))
-        return fail(P1X_EWORKSPACE, "workspace of " + std::to_string(need) + " bytes required");
-    if (need && !aligned(ws, 16)) return fail(P1X_EINVAL, "workspace must be 16-byte aligned");
-    const size_t n_part = size_t(p->batch) * p->n_head_q * p->seq_q * a.splits;
-    a.part_o = static_cast<float*>(ws);
-    a.part_ml = reinterpret_cast<float2*>(a.part_o + n_part * d);
-    a.o = o;
-    a.lse = lse;
+    p1x::FaArgs a;
+    if (int rc = fa_prepare(p, q, k, v, strides, mask, nullptr, o, lse, ws, ws_bytes, a)) return rc;
     hipError_t e = p1x::launch_fa_decode(a, p->batch, p->d_qk, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? P1X_OK : hip_fail(e, "flash_attn_decode");
+}
+
+int p1x_flash_attn_decode_kvlen(const p1x_attn_params* p, const float* q, const uint16_t* k, const uint16_t* v,
+                                const p1x_kv_strides* strides, const float* mask, const int32_t* kv_len, float* o,
+                                float* lse, void* ws, size_t ws_bytes, void* stream) {
+    if (int rc = ensure_init()) return rc;
+    if (!kv_len) return fail(P1X_EINVAL, "null kv_len pointer");
+    if (!aligned(kv_len, 4)) return fail(P1X_EINVAL, "kv_len must be 4-byte aligned");
+    p1x::FaArgs a;
+    if (int rc = fa_prepare(p, q, k, v, strides, mask, kv_len, o, lse, ws, ws_bytes, a)) return rc;
+    hipError_t e = p1x::launch_fa_decode(a, p->batch, p->d_qk, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? P1X_OK : hip_fail(e, "flash_attn_decode_kvlen");
 }
 
 int p1x_round_to_fp16(const float* x, uint16_t* out, int64_t n, void* stream) {

@@ -115,6 +115,38 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
 }
 __device__ __forceinline__ float round_fp16(float x) { return __half2float(__float2half(x)); }
 
+// Reductions over the 32 lanes of a wave half (one 32-element activation block): the xor butterfly with offsets
+// 16, 8, 4, 2, 1, the exact FP32 order of the reference (src/reference/qmv_model.cpp:44-52). Since a+b == b+a in
+// IEEE arithmetic, every lane of the half ends with the same, order-defined result.
+__device__ __forceinline__ float half_max32(float v) {
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ float half_sum32(float v) {
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ int half_isum32(int v) {
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// Q8_1 of one activation element per lane, the 32 lanes of a wave half holding one whole block (element i of
+// the column, i % 32 == lane % 32) (qmv_model.cpp:60-68, quantize.cu:88-110): d = amax/127 (IEEE division),
+// q = round(x/d) with ties away from zero, s = fp16(butterfly sum of x), isum = the exact sum of q.
+__device__ __forceinline__ void q8_1_store(float v, int64_t i, int8_t* __restrict__ qs, float4* __restrict__ ds) {
+    const float amax = half_max32(fabsf(v));
+    const float d = amax / 127.0f;
+    const int q = amax == 0.0f ? 0 : static_cast<int>(roundf(v / d));
+    qs[i] = static_cast<int8_t>(q);
+    const float s = half_sum32(v);
+    const int isum = half_isum32(q);
+    if ((i & 31) == 0) ds[i / 32] = make_float4(round_fp16(d), round_fp16(s), static_cast<float>(isum), 0.0f);
+}
+
 // Sum over the 64 lanes of a wave; every lane gets the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

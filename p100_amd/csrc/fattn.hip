@@ -140,8 +140,10 @@ __global__ __launch_bounds__(256) void k_fa_split(FaArgs a) {
     // covers the same 1/CH slice of GPW consecutive rows (whole 128-byte lines).
     auto dim0 = [&](int c) { return c * (D / CH) + 8 * l; };
 
-    // Visible keys [0, j_end); this work-group's share [j0, j1).
-    const int j_end = a.causal ? min(a.seq_kv, i + (a.seq_kv - a.seq_q) + 1) : a.seq_kv;
+    // Visible keys [0, j_end); this work-group's share [j0, j1). With a device-side length the cache holds
+    // n_kv <= seq_kv valid rows at execution time (the split plan covers all seq_kv).
+    const int n_kv = a.kv_len ? min(max(*a.kv_len, 0), a.seq_kv) : a.seq_kv;
+    const int j_end = a.causal ? min(n_kv, i + (n_kv - a.seq_q) + 1) : n_kv;
     const int j0 = split * a.chunk;
     const int j1 = min(j0 + a.chunk, j_end);
 
@@ -487,7 +489,7 @@ int fa_heads_per_wg(int hq, int hkv) {
     return 1;
 }
 
-// KV split: chunks of whole work-group batches (4 waves x 64/(d/16) groups x 2 keys), about
+// KV split: chunks of whole work-group batches (kWaves waves x 64/(d/kDimsPerLane) groups x kKeys keys), about
 // P1X_FA_TARGET_WGS pass-1 work-groups in total, at most kMaxSplits splits.
 void fa_split_plan(int batch, int hq, int hkv, int seq_q, int seq_kv, int d, int& splits, int& chunk) {
     const int kpb = kWaves * (64 / (d / kDimsPerLane)) * kKeys;

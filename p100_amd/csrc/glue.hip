@@ -1,0 +1,285 @@
+// Decode-step glue around the mat-vec and attention kernels: the element-wise ops of llama.cpp's decode graph
+// for a Llama-architecture model (llm_build_llama at batch 1): get_rows, rms_norm + mul, rope + the KV-cache
+// copy, swiglu and argmax. Each is fused with its neighbour where the next op would re-read the same vector:
+// RMSNorm takes the residual add in and emits the Q8_1 activation of the next mat-vec, SwiGLU emits the Q8_1
+// activation of the down projection, RoPE writes K and V straight into the fp16 cache.
+//
+// All are tiny and latency-bound (a few KB to 0.5 MB per launch); they are shaped for few dependent memory
+// round trips, not for bandwidth. Device-resident decode state (DecodeState) lets one captured graph of a whole
+// token step be replayed at every position: the position, the prompt length and the visible KV length are read
+// from device memory when the kernels run.
+#include "common.h"
+#include "launch.h"
+
+namespace p1x {
+namespace {
+
+// ---------------------------------------------------------------------------------------------- get_rows
+// out[i] = deq(w[row])[i] for q4_0 (d * (q - 8), q the nibble) or q8_0 (d * q), ggml's dequantize_q4_0 /
+// dequantize_q8_0. Row index: *row_dev, or (DECODE) the token of the state's position: prompt[pos] while the
+// prompt lasts, else the model's own prediction tokens[pos]; an index outside [0, n_rows) reads row 0.
+// DECODE also publishes the visible KV length of this step, n_kv = min(pos + 1, n_ctx), for the attention.
+template <int TYPE, bool DECODE>
+__global__ __launch_bounds__(256) void k_get_rows(const uint8_t* __restrict__ w, int64_t nb01, int n_rows, int K,
+                                                  const int* __restrict__ row_dev, DecodeState* st,
+                                                  const int* __restrict__ prompt, const int* __restrict__ tokens,
+                                                  int n_ctx, float* __restrict__ out) {
+    int row;
+    if constexpr (DECODE) {
+        const int pos = st->pos;
+        row = pos < 0 ? 0 : (pos < st->n_prompt ? prompt[pos] : (pos <= n_ctx ? tokens[pos] : 0));
+        if (blockIdx.x == 0 && threadIdx.x == 0) st->n_kv = pos < 0 ? 0 : (pos + 1 < n_ctx ? pos + 1 : n_ctx);
+    } else {
+        row = *row_dev;
+    }
+    if (row < 0 || row >= n_rows) row = 0;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= K) return;
+    const uint8_t* blk = w + size_t(row) * nb01 + size_t(i / 32) * (TYPE == Q4_0 ? 18 : 34);
+    const float d = half_bits_to_float(uint32_t(blk[0]) | (uint32_t(blk[1]) << 8));
+    const int j = i % 32;
+    float q;
+    if constexpr (TYPE == Q4_0) {
+        const uint32_t b = blk[2 + (j & 15)];
+        q = float(int(j < 16 ? (b & 15u) : (b >> 4)) - 8);
+    } else {
+        q = float(static_cast<int8_t>(blk[2 + j]));
+    }
+    out[i] = q * d;
+}
+
+// ---------------------------------------------------------------------------------------------- rms_norm
+constexpr int kNormThreads = 1024;
+constexpr int kNormMaxPasses = 16;  // n <= 16384
+
+// One work-group: x += add (when add is given; x is the residual stream and is written back), then
+// h = (x * rsqrt(mean(x^2) + eps)) * w (ggml rms_norm then mul, the CUDA backend's fused rms_norm_mul order),
+// then the Q8_1 activation of h (and h itself when h_out is given). n % 32 == 0.
+__global__ __launch_bounds__(kNormThreads) void k_rms_norm_q8_1(float* __restrict__ x, const float* __restrict__ add,
+                                                               const float* __restrict__ w, int n, float eps,
+                                                               int8_t* __restrict__ qs, float4* __restrict__ ds,
+                                                               float* __restrict__ h_out) {
+    __shared__ float part[kNormThreads / kWave];
+    const int t = threadIdx.x;
+    float v[kNormMaxPasses];
+    float ss = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kNormMaxPasses; ++r) {
+        const int i = r * kNormThreads + t;
+        v[r] = 0.0f;
+        if (i < n) {
+            float xv = x[i];
+            if (add) {
+                xv += add[i];
+                x[i] = xv;
+            }
+            v[r] = xv;
+            ss = fmaf(xv, xv, ss);
+        }
+    }
+    ss = wave_sum(ss);
+    if ((t & 63) == 0) part[t >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kNormThreads / kWave; ++k) tot += part[k];
+    const float scale = rsqrtf(tot / float(n) + eps);
+#pragma unroll
+    for (int r = 0; r < kNormMaxPasses; ++r) {
+        const int i = r * kNormThreads + t;
+        if (i < n) {  // whole 32-lane halves: n % 32 == 0 and i % 32 == t % 32
+            const float hv = (v[r] * scale) * w[i];
+            if (h_out) h_out[i] = hv;
+            q8_1_store(hv, i, qs, ds);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------- swiglu
+// h = silu(gate) * up, silu(g) = g / (1 + exp(-g)) (ggml's swiglu), then the Q8_1 activation of h.
+__global__ __launch_bounds__(256) void k_swiglu_q8_1(const float* __restrict__ gate, const float* __restrict__ up,
+                                                     int n, int8_t* __restrict__ qs, float4* __restrict__ ds,
+                                                     float* __restrict__ h_out) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;  // whole 32-lane halves: n % 32 == 0
+    const float g = gate[i];
+    const float hv = g / (1.0f + expf(-g)) * up[i];
+    if (h_out) h_out[i] = hv;
+    q8_1_store(hv, i, qs, ds);
+}
+
+// ---------------------------------------------------------------------------------------------- rope + KV append
+// Rotary embedding of llama.cpp's "normal" mode (adjacent pairs, rope_norm in rope.cu): for pair p of a head,
+// theta = pos * theta_scale^p with theta_scale = base^(-2/head_dim); (x0, x1) -> (x0 cos - x1 sin,
+// x0 sin + x1 cos). Threads [0, n_head*d/2) rotate q into q_out; the next n_head_kv*d/2 rotate k and store it
+// as fp16 at row pos of the K cache; the last n_head_kv*d/2 store v as fp16 at row pos of the V cache
+// (the cache layout is [n_head_kv][n_ctx][d]). A position outside [0, n_ctx) writes no cache row.
+__global__ __launch_bounds__(256) void k_rope_kv_append(const float* __restrict__ q, const float* __restrict__ k,
+                                                        const float* __restrict__ v, float* __restrict__ q_out,
+                                                        __half* __restrict__ k_cache, __half* __restrict__ v_cache,
+                                                        int n_head, int n_head_kv, int d, int n_ctx,
+                                                        const int* __restrict__ pos_dev, float theta_scale) {
+    const int half = d / 2;
+    const int nq = n_head * half, nk = n_head_kv * half;
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    if (t >= nq + 2 * nk) return;
+    const int pos = *pos_dev;
+    const bool row_ok = pos >= 0 && pos < n_ctx;
+    if (t >= nq + nk) {  // V: copy
+        const int u = t - nq - nk, h = u / half, p = u % half;
+        if (!row_ok) return;
+        const float2 x = *reinterpret_cast<const float2*>(v + size_t(h) * d + 2 * p);
+        *reinterpret_cast<__half2*>(v_cache + (size_t(h) * n_ctx + pos) * d + 2 * p) = __floats2half2_rn(x.x, x.y);
+        return;
+    }
+    const bool is_q = t < nq;
+    const int u = is_q ? t : t - nq, h = u / half, p = u % half;
+    const float2 x = *reinterpret_cast<const float2*>((is_q ? q : k) + size_t(h) * d + 2 * p);
+    const float theta = float(pos) * powf(theta_scale, float(p));
+    const float c = cosf(theta), s = sinf(theta);
+    const float y0 = x.x * c - x.y * s, y1 = x.x * s + x.y * c;
+    if (is_q) {
+        *reinterpret_cast<float2*>(q_out + size_t(h) * d + 2 * p) = make_float2(y0, y1);
+    } else if (row_ok) {
+        *reinterpret_cast<__half2*>(k_cache + (size_t(h) * n_ctx + pos) * d + 2 * p) = __floats2half2_rn(y0, y1);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------- argmax
+// Index of the largest value (the first one on ties; NaN never wins), ggml's argmax. Pass 1: each of G
+// work-groups scans a contiguous slice; pass 2 (one work-group) reduces the G candidates.
+struct Cand {
+    float v;
+    int i;
+};
+__device__ __forceinline__ Cand better(Cand a, Cand b) {  // a precedes b in index order when both are valid
+    if (b.i < 0) return a;
+    if (a.i < 0) return b;
+    return (b.v > a.v || (b.v == a.v && b.i < a.i)) ? b : a;
+}
+__device__ __forceinline__ Cand wave_best(Cand c) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        Cand other{__shfl_xor(c.v, o), __shfl_xor(c.i, o)};
+        c = better(c, other);
+    }
+    return c;
+}
+__device__ __forceinline__ Cand block_best(Cand c) {  // 256 threads; every thread gets the result
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    c = wave_best(c);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        sv[wave] = c.v;
+        si[wave] = c.i;
+    }
+    __syncthreads();
+    Cand r{sv[0], si[0]};
+#pragma unroll
+    for (int k = 1; k < 4; ++k) r = better(r, Cand{sv[k], si[k]});
+    return r;
+}
+
+__global__ __launch_bounds__(256) void k_argmax_partial(const float* __restrict__ x, int n, int per_wg,
+                                                        Cand* __restrict__ part) {
+    const int lo = blockIdx.x * per_wg, hi = min(n, lo + per_wg);
+    Cand c{-INFINITY, -1};
+    for (int i = lo + threadIdx.x; i < hi; i += 256) {
+        const float v = x[i];
+        if (v == v && (c.i < 0 || v > c.v)) c = Cand{v, i};  // ascending i per thread: strict > keeps the first
+    }
+    c = block_best(c);
+    if (threadIdx.x == 0) part[blockIdx.x] = c;
+}
+
+// Reduces the candidates. out (optional) gets the index (or -1 if every value is NaN, as no index wins).
+// With a decode state, the index is the prediction for position pos + 1: it is stored at tokens[pos + 1] and the
+// state advances to pos + 1 (a position outside [0, n_ctx) neither stores nor advances).
+__global__ __launch_bounds__(256) void k_argmax_final(const Cand* __restrict__ part, int g, int* __restrict__ out,
+                                                      DecodeState* st, int* __restrict__ tokens, int n_ctx) {
+    Cand c{-INFINITY, -1};
+    for (int k = threadIdx.x; k < g; k += 256) c = better(c, part[k]);
+    c = block_best(c);
+    if (threadIdx.x != 0) return;
+    if (out) *out = c.i;
+    if (st) {
+        const int pos = st->pos;
+        if (pos >= 0 && pos < n_ctx) {
+            tokens[pos + 1] = c.i < 0 ? 0 : c.i;
+            st->pos = pos + 1;
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_get_rows(int type, const void* w, int64_t nb01, int n_rows, int K, const int* row_dev, float* out,
+                           hipStream_t stream) {
+    const dim3 grid((K + 255) / 256);
+    const auto* wb = static_cast<const uint8_t*>(w);
+    if (type == Q4_0)
+        hipLaunchKernelGGL((k_get_rows<Q4_0, false>), grid, dim3(256), 0, stream, wb, nb01, n_rows, K, row_dev,
+                           nullptr, nullptr, nullptr, 0, out);
+    else
+        hipLaunchKernelGGL((k_get_rows<Q8_0, false>), grid, dim3(256), 0, stream, wb, nb01, n_rows, K, row_dev,
+                           nullptr, nullptr, nullptr, 0, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_embed(int type, const void* w, int64_t nb01, int n_rows, int K, DecodeState* st,
+                               const int* prompt, const int* tokens, int n_ctx, float* out, hipStream_t stream) {
+    const dim3 grid((K + 255) / 256);
+    const auto* wb = static_cast<const uint8_t*>(w);
+    if (type == Q4_0)
+        hipLaunchKernelGGL((k_get_rows<Q4_0, true>), grid, dim3(256), 0, stream, wb, nb01, n_rows, K, nullptr, st,
+                           prompt, tokens, n_ctx, out);
+    else
+        hipLaunchKernelGGL((k_get_rows<Q8_0, true>), grid, dim3(256), 0, stream, wb, nb01, n_rows, K, nullptr, st,
+                           prompt, tokens, n_ctx, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_norm_q8_1(float* x, const float* add, const float* w, int n, float eps, int8_t* qs, float* ds,
+                                float* h_out, hipStream_t stream) {
+    hipLaunchKernelGGL(k_rms_norm_q8_1, dim3(1), dim3(kNormThreads), 0, stream, x, add, w, n, eps, qs,
+                       reinterpret_cast<float4*>(ds), h_out);
+    return hipGetLastError();
+}
+int rms_norm_max_n() { return kNormThreads * kNormMaxPasses; }
+
+hipError_t launch_swiglu_q8_1(const float* gate, const float* up, int n, int8_t* qs, float* ds, float* h_out,
+                              hipStream_t stream) {
+    hipLaunchKernelGGL(k_swiglu_q8_1, dim3((n + 255) / 256), dim3(256), 0, stream, gate, up, n, qs,
+                       reinterpret_cast<float4*>(ds), h_out);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_kv_append(const float* q, const float* k, const float* v, float* q_out, uint16_t* k_cache,
+                                 uint16_t* v_cache, int n_head, int n_head_kv, int d, int n_ctx, const int* pos_dev,
+                                 float theta_scale, hipStream_t stream) {
+    const int threads = (n_head + 2 * n_head_kv) * (d / 2);
+    hipLaunchKernelGGL(k_rope_kv_append, dim3((threads + 255) / 256), dim3(256), 0, stream, q, k, v, q_out,
+                       reinterpret_cast<__half*>(k_cache), reinterpret_cast<__half*>(v_cache), n_head, n_head_kv, d,
+                       n_ctx, pos_dev, theta_scale);
+    return hipGetLastError();
+}
+
+// Pass-1 work-groups of the argmax: at most 256, each scanning at least 256 values.
+int argmax_groups(int64_t n) {
+    const int64_t g = (n + 255) / 256;
+    return int(g < 1 ? 1 : (g > 256 ? 256 : g));
+}
+size_t argmax_workspace(int64_t n) { return size_t(argmax_groups(n)) * 8; }
+
+hipError_t launch_argmax(const float* x, int n, void* ws, int* out, DecodeState* st, int* tokens, int n_ctx,
+                         hipStream_t stream) {
+    const int g = argmax_groups(n);
+    const int per = (n + g - 1) / g;
+    auto* part = static_cast<Cand*>(ws);
+    hipLaunchKernelGGL(k_argmax_partial, dim3(g), dim3(256), 0, stream, x, n, per, part);
+    hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, stream, part, g, out, st, tokens, n_ctx);
+    return hipGetLastError();
+}
+
+}  // namespace p1x

@@ -27,6 +27,7 @@ struct FaArgs {
     float2* part_ml;  // [groups][splits][NH]: base-2 max and sum of each split
     float* o;
     float* lse;
+    const int* kv_len;  // optional device int: valid KV rows at execution time (<= seq_kv); null = seq_kv
     int64_t k_row, k_head, k_batch, v_row, v_head, v_batch;  // element strides
     uint32_t k_bytes, v_bytes;  // bytes spanned by one head's seq_kv rows of K and of V
     int hq, hkv, seq_q, seq_kv, causal, splits, chunk, head_chunks;
@@ -35,5 +36,27 @@ struct FaArgs {
 hipError_t launch_fa_decode(FaArgs a, int batch, int d, hipStream_t stream);
 int fa_heads_per_wg(int hq, int hkv);
 void fa_split_plan(int batch, int hq, int hkv, int seq_q, int seq_kv, int d, int& splits, int& chunk);
+
+// Decode-step glue (glue.hip). Device-resident state of a greedy decode: the position being decoded, the
+// prompt length, and the visible KV length of the current step (published by the embedding kernel).
+struct DecodeState {
+    int pos, n_prompt, n_kv, reserved;
+};
+hipError_t launch_get_rows(int type, const void* w, int64_t nb01, int n_rows, int K, const int* row_dev, float* out,
+                           hipStream_t stream);
+hipError_t launch_decode_embed(int type, const void* w, int64_t nb01, int n_rows, int K, DecodeState* st,
+                               const int* prompt, const int* tokens, int n_ctx, float* out, hipStream_t stream);
+hipError_t launch_rms_norm_q8_1(float* x, const float* add, const float* w, int n, float eps, int8_t* qs, float* ds,
+                                float* h_out, hipStream_t stream);
+int rms_norm_max_n();
+hipError_t launch_swiglu_q8_1(const float* gate, const float* up, int n, int8_t* qs, float* ds, float* h_out,
+                              hipStream_t stream);
+hipError_t launch_rope_kv_append(const float* q, const float* k, const float* v, float* q_out, uint16_t* k_cache,
+                                 uint16_t* v_cache, int n_head, int n_head_kv, int d, int n_ctx, const int* pos_dev,
+                                 float theta_scale, hipStream_t stream);
+int argmax_groups(int64_t n);
+size_t argmax_workspace(int64_t n);
+hipError_t launch_argmax(const float* x, int n, void* ws, int* out, DecodeState* st, int* tokens, int n_ctx,
+                         hipStream_t stream);
 
 }  // namespace p1x

@@ -54,3 +54,65 @@ def test_version_without_gpu():
     syms = p100_amd.load_symbols_only()
     syms["p1x_version"].restype = int
     assert syms["p1x_version"]() >= 100
+
+
+def test_struct_layouts_match_header(tmp_path):
+    """The ctypes mirrors have the C structs' sizes and field offsets (compiled from include/p1x.h with gcc)."""
+    import ctypes as C
+
+    import p100_amd
+    from p100_amd import llama
+
+    structs = {
+        "p1x_attn_params": (p100_amd.AttnParams, [f for f, _ in p100_amd.AttnParams._fields_]),
+        "p1x_kv_strides": (p100_amd.KVStrides, [f for f, _ in p100_amd.KVStrides._fields_]),
+        "p1x_llama_hparams": (llama.LlamaHParams, [f for f, _ in llama.LlamaHParams._fields_]),
+        "p1x_llama_layer": (llama.LlamaLayer, [f for f, _ in llama.LlamaLayer._fields_]),
+        "p1x_llama_model": (llama.LlamaModelC, [f for f, _ in llama.LlamaModelC._fields_]),
+    }
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "p1x.h"', "int main(void) {"]
+    for name, (_, fields) in structs.items():
+        lines.append(f'printf("{name} size %zu\\n", sizeof({name}));')
+        for f in fields:
+            lines.append(f'printf("{name} {f} %zu\\n", offsetof({name}, {f}));')
+    lines.append('printf("p1x_decode_state size %zu\\n", sizeof(p1x_decode_state));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    got = {}
+    for ln in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines():
+        *key, val = ln.split()
+        got[tuple(key)] = int(val)
+    for name, (cls, fields) in structs.items():
+        assert got[(name, "size")] == C.sizeof(cls), name
+        for f in fields:
+            assert got[(name, f)] == getattr(cls, f).offset, (name, f)
+    assert got[("p1x_decode_state", "size")] == 16
+
+
+def test_llama_workspace_without_gpu():
+    """Workspace sizing is host arithmetic: 0 for invalid hyper-parameters, room for every buffer otherwise."""
+    import ctypes as C
+
+    import p100_amd
+    from p100_amd import llama
+
+    syms = p100_amd.load_symbols_only()
+    ws = syms["p1x_llama_workspace"]
+    ws.restype, ws.argtypes = C.c_size_t, [C.c_void_p]
+    hp = llama.hparams(768)
+    n = ws(C.byref(hp))
+    E, F, V = 4096, 14336, 128256
+    assert n >= (4 * E + (E + 2 * 1024) + 2 * F + V) * 4 + F + F // 32 * 16
+    assert n < 64 << 20
+    bad = [dict(n_head=3), dict(n_embd=96 * 32, n_head=32), dict(n_ff=100), dict(n_embd=32768, n_head=256),
+           dict(n_layer=0)]
+    for kw in bad:
+        assert ws(C.byref(llama.hparams(768, **kw))) == 0, kw
+    assert ws(C.byref(llama.hparams(768, embd_type=p100_amd.Q4_K))) == 0
+    assert ws(C.byref(llama.hparams(768, wtype=p100_amd.Q4_K, output_type=p100_amd.Q6_K))) > 0
+    am = syms["p1x_argmax_workspace"]
+    am.restype, am.argtypes = C.c_size_t, [C.c_int64]
+    assert am(1) == 8 and am(128256) == 256 * 8 and am(0) == 0
