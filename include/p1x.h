@@ -155,11 +155,12 @@ int p1x_get_rows(int wtype, const void* w, int64_t nb01, int64_t n_rows, int64_t
 
 /* x[i] += add[i] when add is not NULL (x, the residual stream, is updated in place); then
  * h = (x * rsqrt(mean(x^2) + eps)) * w and its Q8_1 activation (qs, ds as p1x_quantize_q8_1, one column).
- * h_out (f32 [n]) optional. n % 32 == 0, n <= 16384. */
+ * h_out (f32 [n]) optional. n % 32 == 0, n <= 16384; every pointer 16-byte aligned. */
 int p1x_rms_norm_q8_1(float* x, const float* add, const float* w, int64_t n, float eps, int8_t* qs, float* ds,
                       float* h_out, void* stream);
 
-/* h = silu(gate) * up with silu(g) = g / (1 + exp(-g)), and its Q8_1 activation; h_out optional. n % 32 == 0. */
+/* h = silu(gate) * up with silu(g) = g / (1 + exp(-g)), and its Q8_1 activation; h_out optional. n % 32 == 0;
+ * every pointer 16-byte aligned. */
 int p1x_swiglu_q8_1(const float* gate, const float* up, int64_t n, int8_t* qs, float* ds, float* h_out, void* stream);
 
 /* Rotary embedding, llama.cpp's normal mode: pair p = (x[2p], x[2p+1]) of each head rotates by

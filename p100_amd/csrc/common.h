@@ -147,6 +147,56 @@ __device__ __forceinline__ void q8_1_store(float v, int64_t i, int8_t* __restric
     if ((i & 31) == 0) ds[i / 32] = make_float4(round_fp16(d), round_fp16(s), static_cast<float>(isum), 0.0f);
 }
 
+// DPP exchanges inside a quad of lanes: the value of lane ^ 1 and of lane ^ 2.
+__device__ __forceinline__ int quad_xor1_i(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, true); }
+__device__ __forceinline__ int quad_xor2_i(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, true); }
+__device__ __forceinline__ float quad_xor1(float v) {
+    return __builtin_bit_cast(float, quad_xor1_i(__builtin_bit_cast(int, v)));
+}
+__device__ __forceinline__ float quad_xor2(float v) {
+    return __builtin_bit_cast(float, quad_xor2_i(__builtin_bit_cast(int, v)));
+}
+
+// Q8_1 of a 32-element block held by a quad of lanes, 8 consecutive elements per lane (lane t of the quad holds
+// elements 8t..8t+7), with the arithmetic of q8_1_store: d = amax/127 and q = round(x/d) (IEEE division), and
+// the sum s in the reference's butterfly order exactly (offsets 16 and 8 are the lane bits 1 and 0 of the quad,
+// exchanged by DPP; offsets 4, 2, 1 are inside the lane). Every lane gets d, s and isum; q holds its 8 codes as
+// two little-endian dwords.
+struct Q81Quad {
+    uint32_t q0, q1;
+    float d, s;
+    int isum;
+};
+__device__ __forceinline__ Q81Quad q8_1_quad(const float v[8]) {
+    float m = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[e]));
+    m = fmaxf(m, quad_xor1(m));
+    m = fmaxf(m, quad_xor2(m));
+    const float d = m / 127.0f;
+    int q[8], isum = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        q[e] = m == 0.0f ? 0 : static_cast<int>(roundf(v[e] / d));
+        isum += q[e];
+    }
+    isum += quad_xor1_i(isum);
+    isum += quad_xor2_i(isum);
+    float t[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = v[e] + quad_xor2(v[e]);  // offset 16 (element bit 4)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = t[e] + quad_xor1(t[e]);  // offset 8 (bit 3)
+    const float w0 = t[0] + t[4], w1 = t[1] + t[5], w2 = t[2] + t[6], w3 = t[3] + t[7];  // offset 4
+    Q81Quad r;
+    r.s = (w0 + w2) + (w1 + w3);  // offsets 2, 1
+    r.d = d;
+    r.isum = isum;
+    r.q0 = (uint32_t(q[0]) & 255) | (uint32_t(q[1]) & 255) << 8 | (uint32_t(q[2]) & 255) << 16 | uint32_t(q[3]) << 24;
+    r.q1 = (uint32_t(q[4]) & 255) | (uint32_t(q[5]) & 255) << 8 | (uint32_t(q[6]) & 255) << 16 | uint32_t(q[7]) << 24;
+    return r;
+}
+
 // Sum over the 64 lanes of a wave; every lane gets the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -100,7 +100,9 @@ int p1x_rms_norm_q8_1(float* x, const float* add, const float* w, int64_t n, flo
     if (n <= 0 || n % 32 || n > p1x::rms_norm_max_n())
         return fail(P1X_EINVAL, "n must be a positive multiple of 32, at most 16384");
     if (!(eps >= 0.0f) || !std::isfinite(eps)) return fail(P1X_EINVAL, "eps must be finite and non-negative");
-    if (!aligned(qs, 16) || !aligned(ds, 16)) return fail(P1X_EINVAL, "qs and ds must be 16-byte aligned");
+    if (!aligned(qs, 16) || !aligned(ds, 16) || !aligned(x, 16) || !aligned(add, 16) || !aligned(w, 16) ||
+        !aligned(h_out, 16))
+        return fail(P1X_EINVAL, "x, add, w, h_out, qs and ds must be 16-byte aligned");
     hipError_t e = p1x::launch_rms_norm_q8_1(x, add, w, int(n), eps, qs, ds, h_out, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? P1X_OK : hip_fail(e, "rms_norm_q8_1");
 }
@@ -109,7 +111,8 @@ int p1x_swiglu_q8_1(const float* gate, const float* up, int64_t n, int8_t* qs, f
     if (int rc = ensure_init()) return rc;
     if (!gate || !up || !qs || !ds) return fail(P1X_EINVAL, "null pointer");
     if (n <= 0 || n % 32 || n > INT32_MAX) return fail(P1X_EINVAL, "n must be a positive multiple of 32");
-    if (!aligned(qs, 16) || !aligned(ds, 16)) return fail(P1X_EINVAL, "qs and ds must be 16-byte aligned");
+    if (!aligned(qs, 16) || !aligned(ds, 16) || !aligned(gate, 16) || !aligned(up, 16) || !aligned(h_out, 16))
+        return fail(P1X_EINVAL, "gate, up, h_out, qs and ds must be 16-byte aligned");
     hipError_t e = p1x::launch_swiglu_q8_1(gate, up, int(n), qs, ds, h_out, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? P1X_OK : hip_fail(e, "swiglu_q8_1");
 }
@@ -163,12 +166,15 @@ int p1x_llama_decode_step(const p1x_llama_model* m, p1x_decode_state* state, con
         if (!L.attn_norm || !L.wq || !L.wk || !L.wv || !L.wo || !L.ffn_norm || !L.w_gate || !L.w_up || !L.w_down ||
             !L.k_cache || !L.v_cache)
             return fail(P1X_EINVAL, "layer " + std::to_string(l) + " has a null pointer");
+        if (!aligned(L.attn_norm, 16) || !aligned(L.ffn_norm, 16))
+            return fail(P1X_EINVAL, "layer " + std::to_string(l) + ": norm weights must be 16-byte aligned");
         if (!aligned(L.k_cache, 16) || !aligned(L.v_cache, 16) || !aligned(L.wq, 4) || !aligned(L.wk, 4) ||
             !aligned(L.wv, 4) || !aligned(L.wo, 4) || !aligned(L.w_gate, 4) || !aligned(L.w_up, 4) ||
             !aligned(L.w_down, 4))
             return fail(P1X_EINVAL, "layer " + std::to_string(l) + ": caches must be 16-byte, weights 4-byte aligned");
     }
-    if (!aligned(m->output, 4) || !aligned(state, 16)) return fail(P1X_EINVAL, "output 4-byte, state 16-byte aligned");
+    if (!aligned(m->output, 4) || !aligned(state, 16) || !aligned(m->output_norm, 16))
+        return fail(P1X_EINVAL, "output 4-byte, state and output norm 16-byte aligned");
     const Layout W = layout(hp);
     if (!ws || ws_bytes < W.total)
         return fail(P1X_EWORKSPACE, "workspace of " + std::to_string(W.total) + " bytes required");

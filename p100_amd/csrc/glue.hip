@@ -49,63 +49,101 @@ __global__ __launch_bounds__(256) void k_get_rows(const uint8_t* __restrict__ w,
 }
 
 // ---------------------------------------------------------------------------------------------- rms_norm
-constexpr int kNormThreads = 1024;
-constexpr int kNormMaxPasses = 16;  // n <= 16384
+// Each lane owns 8 consecutive elements per pass (a quad of lanes holds one Q8_1 block, q8_1_quad), so the block
+// reductions are DPP exchanges and in-lane adds rather than cross-lane shuffles through LDS.
+constexpr int kNormMaxThreads = 1024;
+constexpr int kNormMaxPasses = 2;  // n <= 2 * 8 * 1024 = 16384
 
-// One work-group: x += add (when add is given; x is the residual stream and is written back), then
-// h = (x * rsqrt(mean(x^2) + eps)) * w (ggml rms_norm then mul, the CUDA backend's fused rms_norm_mul order),
-// then the Q8_1 activation of h (and h itself when h_out is given). n % 32 == 0.
-__global__ __launch_bounds__(kNormThreads) void k_rms_norm_q8_1(float* __restrict__ x, const float* __restrict__ add,
-                                                               const float* __restrict__ w, int n, float eps,
-                                                               int8_t* __restrict__ qs, float4* __restrict__ ds,
-                                                               float* __restrict__ h_out) {
-    __shared__ float part[kNormThreads / kWave];
-    const int t = threadIdx.x;
-    float v[kNormMaxPasses];
+__device__ __forceinline__ void load8(const float* p, float v[8]) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+}
+__device__ __forceinline__ void store8(float* p, const float v[8]) {
+    reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+__device__ __forceinline__ void store_q8_1(const Q81Quad& r, int64_t e0, int8_t* __restrict__ qs,
+                                           float4* __restrict__ ds) {
+    *reinterpret_cast<uint2*>(qs + e0) = make_uint2(r.q0, r.q1);
+    if ((e0 & 31) == 0) ds[e0 / 32] = make_float4(round_fp16(r.d), round_fp16(r.s), static_cast<float>(r.isum), 0.0f);
+}
+// Sum over the 64 lanes of a wave, every lane getting it: DPP inside 16-lane rows, then the four row totals.
+__device__ __forceinline__ float wave_total(float v) {
+    v += quad_xor1(v);
+    v += quad_xor2(v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xf, 0xf, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xf, 0xf, true));
+    const int b = __builtin_bit_cast(int, v);
+    return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))) +
+           (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48)));
+}
+
+// One work-group of blockDim.x = min(1024, n/8 rounded up to a wave) threads: x += add (when add is given; x is the
+// residual stream and is written back), then h = (x * rsqrt(mean(x^2) + eps)) * w (ggml rms_norm then mul, the
+// CUDA backend's fused rms_norm_mul order), then the Q8_1 activation of h (and h itself when h_out is given).
+// n % 32 == 0, so the quads past n are whole and sit out.
+__global__ __launch_bounds__(kNormMaxThreads) void k_rms_norm_q8_1(float* __restrict__ x,
+                                                                  const float* __restrict__ add,
+                                                                  const float* __restrict__ w, int n, float eps,
+                                                                  int8_t* __restrict__ qs, float4* __restrict__ ds,
+                                                                  float* __restrict__ h_out) {
+    __shared__ float part[kNormMaxThreads / kWave];
+    const int t = threadIdx.x, nt = blockDim.x;
+    float v[kNormMaxPasses][8];
     float ss = 0.0f;
 #pragma unroll
     for (int r = 0; r < kNormMaxPasses; ++r) {
-        const int i = r * kNormThreads + t;
-        v[r] = 0.0f;
-        if (i < n) {
-            float xv = x[i];
+        const int e0 = (r * nt + t) * 8;
+        if (e0 < n) {
+            load8(x + e0, v[r]);
             if (add) {
-                xv += add[i];
-                x[i] = xv;
+                float a[8];
+                load8(add + e0, a);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[r][e] += a[e];
+                store8(x + e0, v[r]);
             }
-            v[r] = xv;
-            ss = fmaf(xv, xv, ss);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss = fmaf(v[r][e], v[r][e], ss);
         }
     }
-    ss = wave_sum(ss);
+    ss = wave_total(ss);
     if ((t & 63) == 0) part[t >> 6] = ss;
     __syncthreads();
     float tot = 0.0f;
-#pragma unroll
-    for (int k = 0; k < kNormThreads / kWave; ++k) tot += part[k];
+    for (int k = 0; k < nt / kWave; ++k) tot += part[k];
     const float scale = rsqrtf(tot / float(n) + eps);
 #pragma unroll
     for (int r = 0; r < kNormMaxPasses; ++r) {
-        const int i = r * kNormThreads + t;
-        if (i < n) {  // whole 32-lane halves: n % 32 == 0 and i % 32 == t % 32
-            const float hv = (v[r] * scale) * w[i];
-            if (h_out) h_out[i] = hv;
-            q8_1_store(hv, i, qs, ds);
+        const int e0 = (r * nt + t) * 8;
+        if (e0 < n) {  // whole quads: n % 32 == 0
+            float wv[8], hv[8];
+            load8(w + e0, wv);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) hv[e] = (v[r][e] * scale) * wv[e];
+            if (h_out) store8(h_out + e0, hv);
+            store_q8_1(q8_1_quad(hv), e0, qs, ds);
         }
     }
 }
 
 // ---------------------------------------------------------------------------------------------- swiglu
-// h = silu(gate) * up, silu(g) = g / (1 + exp(-g)) (ggml's swiglu), then the Q8_1 activation of h.
+// h = silu(gate) * up, silu(g) = g / (1 + exp(-g)) (ggml's swiglu), then the Q8_1 activation of h; 8 elements
+// per lane, a quad per block.
 __global__ __launch_bounds__(256) void k_swiglu_q8_1(const float* __restrict__ gate, const float* __restrict__ up,
                                                      int n, int8_t* __restrict__ qs, float4* __restrict__ ds,
                                                      float* __restrict__ h_out) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= n) return;  // whole 32-lane halves: n % 32 == 0
-    const float g = gate[i];
-    const float hv = g / (1.0f + expf(-g)) * up[i];
-    if (h_out) h_out[i] = hv;
-    q8_1_store(hv, i, qs, ds);
+    const int e0 = (blockIdx.x * 256 + threadIdx.x) * 8;
+    if (e0 >= n) return;  // whole quads: n % 32 == 0
+    float g[8], u[8], hv[8];
+    load8(gate + e0, g);
+    load8(up + e0, u);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) hv[e] = g[e] / (1.0f + expf(-g[e])) * u[e];
+    if (h_out) store8(h_out + e0, hv);
+    store_q8_1(q8_1_quad(hv), e0, qs, ds);
 }
 
 // ---------------------------------------------------------------------------------------------- rope + KV append
@@ -242,15 +280,17 @@ hipError_t launch_decode_embed(int type, const void* w, int64_t nb01, int n_rows
 
 hipError_t launch_rms_norm_q8_1(float* x, const float* add, const float* w, int n, float eps, int8_t* qs, float* ds,
                                 float* h_out, hipStream_t stream) {
-    hipLaunchKernelGGL(k_rms_norm_q8_1, dim3(1), dim3(kNormThreads), 0, stream, x, add, w, n, eps, qs,
+    const int lanes = (n / 8 + kWave - 1) / kWave * kWave;
+    const int threads = lanes < kNormMaxThreads ? lanes : kNormMaxThreads;
+    hipLaunchKernelGGL(k_rms_norm_q8_1, dim3(1), dim3(threads), 0, stream, x, add, w, n, eps, qs,
                        reinterpret_cast<float4*>(ds), h_out);
     return hipGetLastError();
 }
-int rms_norm_max_n() { return kNormThreads * kNormMaxPasses; }
+int rms_norm_max_n() { return kNormMaxThreads * kNormMaxPasses * 8; }
 
 hipError_t launch_swiglu_q8_1(const float* gate, const float* up, int n, int8_t* qs, float* ds, float* h_out,
                               hipStream_t stream) {
-    hipLaunchKernelGGL(k_swiglu_q8_1, dim3((n + 255) / 256), dim3(256), 0, stream, gate, up, n, qs,
+    hipLaunchKernelGGL(k_swiglu_q8_1, dim3((n / 8 + 255) / 256), dim3(256), 0, stream, gate, up, n, qs,
                        reinterpret_cast<float4*>(ds), h_out);
     return hipGetLastError();
 }

@@ -65,21 +65,11 @@ struct ActLds {
     }
 };
 
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int v) {
-    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, true);
-}
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
-}
-constexpr int kQuadXor1 = 0xB1, kQuadXor2 = 0x4E;  // quad_perm(1,0,3,2), quad_perm(2,3,0,1)
 
 // Q8_1 of B columns of x (f32 [B][K]) into LDS by the whole work-group. A 32-element block is held by a quad of
 // lanes, 8 consecutive elements each (lane t of the quad: elements 8t..8t+7). The arithmetic is that of
-// k_quantize_q8_1 (qmv_model.cpp:60-68): d = amax/127 and q = round(x/d) with IEEE division, and the sum s
-// follows the reference's xor butterfly exactly (offsets 16, 8: lanes ^ 2, ^ 1 of the quad; 4, 2, 1: inside
-// the lane), so the block is bit-identical to the standalone kernel's.
+// k_quantize_q8_1 (qmv_model.cpp:60-68), with the reference's butterfly order for s (q8_1_quad), so the block
+// is bit-identical to the standalone kernel's.
 template <int B>
 __device__ __forceinline__ void quantize_to_lds(const float* __restrict__ x, int K, uint4* lo, uint4* hi, float4* ds) {
     const int nblk = K / 32, per_col = K / 8, nchunk = B * per_col;  // nchunk % 4 == 0: quads stay whole
@@ -91,36 +81,12 @@ __device__ __forceinline__ void quantize_to_lds(const float* __restrict__ x, int
         const float4* src = reinterpret_cast<const float4*>(x + size_t(c) * K + size_t(e8) * 8);
         const float4 a0 = src[0], a1 = src[1];
         const float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-        float m = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[e]));
-        m = fmaxf(m, dpp_f<kQuadXor1>(m));
-        m = fmaxf(m, dpp_f<kQuadXor2>(m));
-        const float d = m / 127.0f;
-        int q[8], isum = 0;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            q[e] = m == 0.0f ? 0 : static_cast<int>(roundf(v[e] / d));
-            isum += q[e];
-        }
-        isum += dpp_i<kQuadXor1>(isum);
-        isum += dpp_i<kQuadXor2>(isum);
-        float t[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) t[e] = v[e] + dpp_f<kQuadXor2>(v[e]);  // offset 16 (element bit 4)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) t[e] = t[e] + dpp_f<kQuadXor1>(t[e]);  // offset 8 (bit 3)
-        const float w0 = t[0] + t[4], w1 = t[1] + t[5], w2 = t[2] + t[6], w3 = t[3] + t[7];  // offset 4
-        const float sum = (w0 + w2) + (w1 + w3);                                               // offsets 2, 1
+        const Q81Quad r = q8_1_quad(v);
         if (ok) {
             const int blk = c * nblk + (e8 >> 2), lt = e8 & 3;
-            const uint32_t p0 = (uint32_t(q[0]) & 255) | (uint32_t(q[1]) & 255) << 8 | (uint32_t(q[2]) & 255) << 16 |
-                                uint32_t(q[3]) << 24;
-            const uint32_t p1 = (uint32_t(q[4]) & 255) | (uint32_t(q[5]) & 255) << 8 | (uint32_t(q[6]) & 255) << 16 |
-                                uint32_t(q[7]) << 24;
             uint2* dst = reinterpret_cast<uint2*>(lt < 2 ? &lo[blk] : &hi[blk]) + (lt & 1);
-            *dst = make_uint2(p0, p1);
-            if (lt == 0) ds[blk] = make_float4(round_fp16(d), round_fp16(sum), static_cast<float>(isum), 0.0f);
+            *dst = make_uint2(r.q0, r.q1);
+            if (lt == 0) ds[blk] = make_float4(round_fp16(r.d), round_fp16(r.s), static_cast<float>(r.isum), 0.0f);
         }
     }
 }
