@@ -1,6 +1,7 @@
 """Builds p100_amd/libp1x.so for gfx950 with hipcc (in-tree, so the library travels with the source tree).
 
     python -m p100_amd.build          # compile every source, link the shared library
+    python -m p100_amd.build --changed  # recompile only sources newer than their objects (or any header)
 """
 from __future__ import annotations
 
@@ -35,10 +36,20 @@ def _compile(src: str) -> pathlib.Path:
     return obj
 
 
-def build(verbose: bool = True) -> pathlib.Path:
+def _stale(src: str) -> bool:
+    obj = OBJ / (src + ".o")
+    if not obj.exists():
+        return True
+    deps = [CSRC / src, *CSRC.glob("*.h"), PKG.parent / "include" / "p1x.h"]
+    return max(d.stat().st_mtime for d in deps) > obj.stat().st_mtime
+
+
+def build(verbose: bool = True, changed_only: bool = False) -> pathlib.Path:
     OBJ.mkdir(exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+    todo = [s for s in SOURCES if _stale(s)] if changed_only else SOURCES
+    with ThreadPoolExecutor(max_workers=min(max(len(todo), 1), os.cpu_count() or 1)) as ex:
+        list(ex.map(_compile, todo))
+    objs = [OBJ / (s + ".o") for s in SOURCES]
     tmp = OUT.with_suffix(".so.tmp")
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -51,4 +62,4 @@ def build(verbose: bool = True) -> pathlib.Path:
 
 
 if __name__ == "__main__":
-    build()
+    build(changed_only="--changed" in sys.argv[1:])

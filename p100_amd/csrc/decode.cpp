@@ -2,7 +2,8 @@
 //
 // The driver enqueues one token of a Llama-architecture model at batch 1 (llama.cpp's llm_build_llama decode
 // graph) on one stream: 10 launches per layer (RMSNorm + Q8_1, q/k/v mat-vec, RoPE + KV append, attention split
-// and combine, o projection with in-kernel Q8_1, RMSNorm + Q8_1, gate/up mat-vec, SwiGLU + Q8_1, down mat-vec)
+// and combine (which also emits the Q8_1 of its output), o projection, RMSNorm + Q8_1, gate/up mat-vec,
+// SwiGLU + Q8_1, down mat-vec)
 // plus embedding, output norm, output projection and a two-pass argmax. Everything that depends on the position
 // (the token, the RoPE angle, the cache row, the attention length, the next position) is read from device memory
 // when the kernels run, so the enqueued work is identical at every position and one HIP graph capture of it can
@@ -193,13 +194,20 @@ int p1x_llama_decode_step(const p1x_llama_model* m, p1x_decode_state* state, con
     const int64_t nb_e = row_bytes(hp.embd_type, E), nb_w = row_bytes(hp.wtype, E), nb_down = row_bytes(hp.wtype, F);
     const int64_t nb_out = row_bytes(hp.output_type, E);
     const float theta_scale = std::pow(hp.rope_base, -2.0f / float(d));
-    const bool wo_fused = p1x::mmvq_fused_fits(1, E, E);
 
     const p1x_attn_params ap = attn_params(hp);
     p1x::FaArgs fa;
     if (int rc = fa_prepare(&ap, qr, m->layers[0].k_cache, m->layers[0].v_cache, nullptr, nullptr, &state->n_kv, ao,
                             nullptr, base + W.fa, W.fa_bytes, fa))
         return rc;
+    // With a split plan the combine pass also writes the Q8_1 activation of the attention output, so the o
+    // projection runs on it directly; otherwise the o projection quantizes in-kernel (or through qs/ds).
+    const bool wo_prepared = fa.splits > 1;
+    if (wo_prepared) {
+        fa.oq = qs;
+        fa.ods = reinterpret_cast<float4*>(ds);
+    }
+    const bool wo_fused = !wo_prepared && p1x::mmvq_fused_fits(1, E, E);
 
     hipError_t e = hipSuccess;
 #define P1X_TRY(call, what)                         \
@@ -226,7 +234,9 @@ int p1x_llama_decode_step(const p1x_llama_model* m, p1x_decode_state* state, con
         fa.k = reinterpret_cast<const __half*>(L.k_cache);
         fa.v = reinterpret_cast<const __half*>(L.v_cache);
         P1X_TRY(p1x::launch_fa_decode(fa, 1, d, s), "attention");
-        if (wo_fused) {
+        if (wo_prepared) {
+            P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, L.wo, nb_w, E, E, qs, ds, nullptr, y, nullptr, s), "o");
+        } else if (wo_fused) {
             P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, L.wo, nb_w, E, E, nullptr, nullptr, ao, y, nullptr, s), "o");
         } else {
             P1X_TRY(p1x::launch_quantize_q8_1(ao, qs, ds, E, 1, s), "o quantize");

@@ -49,7 +49,12 @@ constexpr int kKeys = P1X_FA_KEYS;
 #define P1X_FA_DPL 8  // K/V dimensions per lane (8 or 16)
 #endif
 constexpr int kDimsPerLane = P1X_FA_DPL;
-constexpr int kWaves = 4;        // waves per pass-1 work-group
+#ifndef P1X_FA_WAVES
+#define P1X_FA_WAVES 4  // waves per pass-1 work-group
+#endif
+constexpr int kWaves = P1X_FA_WAVES;
+constexpr int kSplitThreads = 64 * kWaves;
+constexpr int kCombineWaves = 4;  // pass-2 work-group: one output row per wave
 constexpr int kMaxSplits = 256;  // fa_split_plan never exceeds this
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -122,7 +127,7 @@ constexpr float kTau = 8.0f;
 
 // MODE bit 0: additive mask; bit 1: logit softcap. Compile-time, so the plain decode loop carries neither.
 template <int D, int NH, int MODE>
-__global__ __launch_bounds__(256) void k_fa_split(FaArgs a) {
+__global__ __launch_bounds__(kSplitThreads) void k_fa_split(FaArgs a) {
     constexpr bool kMask = (MODE & 1) != 0, kCap = (MODE & 2) != 0;
     constexpr int DPL = kDimsPerLane;   // dimensions per lane: DPL/8 chunks of 8 (one 16-byte load each)
     constexpr int CH = DPL / 8;
@@ -326,7 +331,7 @@ __global__ __launch_bounds__(256) void k_fa_split(FaArgs a) {
     // Work-group partial per head: rebase the 4 waves to their common max. With one split it is the answer.
     const int grp = blockIdx.y * a.seq_q + i;  // (batch, KV head, head chunk, query row)
     const size_t row0 = (size_t(b) * a.hq + h0) * a.seq_q + i;  // output row of head hh: row0 + hh * seq_q
-    for (int idx = threadIdx.x; idx < NH * D; idx += 256) {
+    for (int idx = threadIdx.x; idx < NH * D; idx += kSplitThreads) {
         const int hh = idx / D, d = idx % D;
         float mx = wm[0][hh];
 #pragma unroll
@@ -374,6 +379,44 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v + __shfl_xor(v, 32);
 }
 
+// Q8_1 of an output row held CPL consecutive columns per lane (the combine's layout), for a mat-vec that takes the
+// attention output next: element e of a 32-block sits in lane bits log2(CPL).. and in-lane bits below, and the
+// block sum follows the reference's butterfly order (offsets 16 .. 1; q8_1_store's arithmetic otherwise).
+template <int CPL>
+__device__ __forceinline__ void q8_1_row(const float* v, size_t col0, int8_t* __restrict__ qs, float4* __restrict__ ds) {
+    float m = 0.0f, t[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        m = fmaxf(m, fabsf(v[c]));
+        t[c] = v[c];
+    }
+#pragma unroll
+    for (int off = 16; off >= CPL; off >>= 1) m = fmaxf(m, __shfl_xor(m, off / CPL));
+    const float d = m / 127.0f;
+    int q[CPL], isum = 0;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        q[c] = m == 0.0f ? 0 : static_cast<int>(roundf(v[c] / d));
+        isum += q[c];
+        qs[col0 + c] = static_cast<int8_t>(q[c]);
+    }
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) {
+        if (off >= CPL) {
+            isum += __shfl_xor(isum, off / CPL);
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) t[c] += __shfl_xor(t[c], off / CPL);
+        } else {
+            float u[CPL];
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) u[c] = t[c] + t[c ^ off];
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) t[c] = u[c];
+        }
+    }
+    if (col0 % 32 == 0) ds[col0 / 32] = make_float4(round_fp16(d), round_fp16(t[0]), static_cast<float>(isum), 0.0f);
+}
+
 // Pass 2: one wave per output row (four rows per work-group). Lane l owns columns [CPL l, CPL l + CPL) of every
 // split's partial, so the weighted sum over splits needs no cross-lane reduction; the split maxima and sums
 // are reduced across lanes once. All loads of a round (kRound splits) are issued before any arithmetic.
@@ -383,9 +426,9 @@ template <int D, int NH>
 __global__ __launch_bounds__(256) void k_fa_combine(FaArgs a, int rows) {
     constexpr int CPL = D / 64;  // columns per lane
     constexpr int kRound = 32;   // splits per round of loads
-    __shared__ float wsh[kWaves][kMaxSplits];
+    __shared__ float wsh[kCombineWaves][kMaxSplits];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row = blockIdx.x * kWaves + wave;
+    const int row = blockIdx.x * kCombineWaves + wave;
     if (row >= rows) return;  // whole wave; nothing below synchronizes across waves
     // Output row (b, h, i) -> group of the split pass and head slot hh inside it.
     const int i = row % a.seq_q, bh = row / a.seq_q, h = bh % a.hq, b = bh / a.hq;
@@ -449,23 +492,29 @@ __global__ __launch_bounds__(256) void k_fa_combine(FaArgs a, int rows) {
     }
     const float inv = den == 0.0f ? 0.0f : 1.0f / den;
     float* dst = a.o + size_t(row) * D + CPL * lane;
+    float ov[CPL];
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) dst[c] = den == 0.0f ? 0.0f : acc[c] * inv;
+    for (int c = 0; c < CPL; ++c) {
+        ov[c] = den == 0.0f ? 0.0f : acc[c] * inv;
+        dst[c] = ov[c];
+    }
     if (a.lse && lane == 0) a.lse[row] = den == 0.0f ? -INFINITY : (mx + log2f(den)) * kLn2;
+    if (a.oq) q8_1_row<CPL>(ov, size_t(row) * D + CPL * lane, a.oq, a.ods);
 }
 
 template <int D, int NH>
 hipError_t launch_split(const FaArgs& a, int batch, hipStream_t stream) {
     const dim3 grid(a.splits, batch * a.hkv * a.head_chunks, a.seq_q);
     switch ((a.mask ? 1 : 0) | (a.softcap > 0.0f ? 2 : 0)) {
-        case 0: hipLaunchKernelGGL((k_fa_split<D, NH, 0>), grid, dim3(256), 0, stream, a); break;
-        case 1: hipLaunchKernelGGL((k_fa_split<D, NH, 1>), grid, dim3(256), 0, stream, a); break;
-        case 2: hipLaunchKernelGGL((k_fa_split<D, NH, 2>), grid, dim3(256), 0, stream, a); break;
-        default: hipLaunchKernelGGL((k_fa_split<D, NH, 3>), grid, dim3(256), 0, stream, a); break;
+        case 0: hipLaunchKernelGGL((k_fa_split<D, NH, 0>), grid, dim3(kSplitThreads), 0, stream, a); break;
+        case 1: hipLaunchKernelGGL((k_fa_split<D, NH, 1>), grid, dim3(kSplitThreads), 0, stream, a); break;
+        case 2: hipLaunchKernelGGL((k_fa_split<D, NH, 2>), grid, dim3(kSplitThreads), 0, stream, a); break;
+        default: hipLaunchKernelGGL((k_fa_split<D, NH, 3>), grid, dim3(kSplitThreads), 0, stream, a); break;
     }
     if (a.splits == 1) return hipGetLastError();  // the split pass wrote O and LSE
     const int rows = batch * a.hq * a.seq_q;
-    hipLaunchKernelGGL((k_fa_combine<D, NH>), dim3((rows + kWaves - 1) / kWaves), dim3(256), 0, stream, a, rows);
+    hipLaunchKernelGGL((k_fa_combine<D, NH>), dim3((rows + kCombineWaves - 1) / kCombineWaves), dim3(64 * kCombineWaves),
+                       0, stream, a, rows);
     return hipGetLastError();
 }
 

@@ -28,6 +28,9 @@
 #ifndef P1X_MMVQ_FUSE_MAX
 #define P1X_MMVQ_FUSE_MAX (1L << 21)  // single launch while work-groups x B x K stays at or below this
 #endif
+#ifndef P1X_MMVQ_HOIST
+#define P1X_MMVQ_HOIST 1  // prepared activation: first weight pass requested before the LDS copy
+#endif
 #ifndef P1X_MMVQ_MAX_RW
 #define P1X_MMVQ_MAX_RW 4
 #endif
@@ -292,9 +295,11 @@ __device__ __forceinline__ void copy_to_lds(const int8_t* __restrict__ qs, const
 // Rows r0 .. r0+RW-1 of one wave, pass by pass over K (64 UB units per pass). The weights of pass p+1 are
 // requested before pass p computes, with two register sets used alternately (the loop body is two passes), so
 // every load in the loop body is unconditional and each wait covers exactly the pass about to be used; the
-// last one or two passes run in an epilogue. `prep` runs first (quantize x into LDS, or copy a prepared
-// activation there); every wave, even one past the last row, takes part in it.
-template <int TYPE, int B, int RW, bool SUMS, class Act, class Prep>
+// last one or two passes run in an epilogue (a deeper ring of register sets, with unconditional loads past the
+// row end, measured slower). `prep` runs first (quantize x into LDS, or copy a prepared activation there);
+// every wave, even one past the last row, takes part in it. HOIST issues the first pass of weight loads before
+// `prep`, so the weight stream and the activation copy share one memory round trip.
+template <int TYPE, int B, int RW, bool SUMS, bool HOIST = false, class Act, class Prep>
 __device__ __forceinline__ void mmvq_rows(const Act act, Prep prep, const uint8_t* __restrict__ w, int64_t nb01,
                                           int M, int K, float* __restrict__ y, int32_t* __restrict__ gs) {
     using U = typename UnitOf<TYPE>::T;
@@ -353,11 +358,12 @@ __device__ __forceinline__ void mmvq_rows(const Act act, Prep prep, const uint8_
         }
     };
 
+    U w0[RW][UB], w1[RW][UB];
+    if constexpr (HOIST) load_w(w0, 0);
     prep();
     if (!wave_ok) return;  // the whole wave leaves; nothing below synchronizes across waves
     const int npass = (units + kStep - 1) / kStep;
-    U w0[RW][UB], w1[RW][UB];
-    load_w(w0, 0);
+    if constexpr (!HOIST) load_w(w0, 0);
     int p = 0;
     for (; p + 2 < npass; p += 2) {
         load_w(w1, (p + 1) * kStep);
@@ -400,7 +406,7 @@ __global__ __launch_bounds__(256) void k_mmvq(const uint8_t* __restrict__ w, int
         extern __shared__ uint4 act_lds[];
         const int nblk = K / 32;
         const LdsAct l(act_lds, B, nblk);
-        mmvq_rows<TYPE, B, RW, SUMS>(
+        mmvq_rows<TYPE, B, RW, SUMS, P1X_MMVQ_HOIST != 0>(
             ActLds{l.lo, l.hi, l.ds, nblk},
             [&] {
                 copy_to_lds<B>(xq, xds, K, l.lo, l.hi, l.ds);

@@ -317,11 +317,11 @@ class RefLlama:
         return self.mv(hp.output_type, self.out, hp.n_vocab, E, self.norm(x, self.out_norm))
 
 
-def tiny_model(wtype, output_type, n_ctx, seed=0, embd_type=2):
+def tiny_model(wtype, output_type, n_ctx, seed=0, embd_type=2, head_dim=64):
     from p100_amd import llama
 
-    hp = llama.hparams(n_ctx, wtype=wtype, embd_type=embd_type, output_type=output_type, n_layer=2, n_embd=256,
-                       n_head=4, n_head_kv=2, n_ff=512, n_vocab=1000)
+    hp = llama.hparams(n_ctx, wtype=wtype, embd_type=embd_type, output_type=output_type, n_layer=2,
+                       n_embd=4 * head_dim, n_head=4, n_head_kv=2, n_ff=512, n_vocab=1000)
     return llama.LlamaModel(hp, device="cuda", seed=seed, std=0.05)
 
 
@@ -344,7 +344,9 @@ def compose_step(model, tok, pos, caches):
         qr = P.rope_kv_append(qkv[:E].reshape(H, d), qkv[E:E + kv].reshape(HKV, d), qkv[E + kv:].reshape(HKV, d),
                               kc, vc, dev_i32(pos), rope_base=hp.rope_base)
         o, _ = P.flash_attn_decode(p, qr.reshape(-1), kc, vc, kv_len=n_kv, want_lse=False)
-        y = P.mul_mat_vec(hp.wtype, L["wo"], E, E, o.reshape(1, E))[0]
+        # a split plan hands the o projection a prepared Q8_1 activation; one split, the in-kernel quantization
+        o_in = P.quantize_q8_1(o.reshape(1, E)) if P.flash_attn_decode_workspace(p) > 0 else o.reshape(1, E)
+        y = P.mul_mat_vec(hp.wtype, L["wo"], E, E, o_in)[0]
         act = P.rms_norm_q8_1(x, L["ffn_norm"], hp.rms_eps, add=y)
         gu = P.mul_mat_vec(hp.wtype, L["w_gate_up"], 2 * F, E, act)[0]
         act = P.swiglu_q8_1(gu[:F], gu[F:])
@@ -354,18 +356,19 @@ def compose_step(model, tok, pos, caches):
     return logits, int(P.argmax(logits).item())
 
 
-CASES = [(2, 2, 2, 40), (8, 8, 8, 300), (12, 14, 2, 300)]
+# (layer type, output type, embedding type, KV capacity, head_dim): one split and several, d 64 / 128 / 256
+CASES = [(2, 2, 2, 40, 64), (8, 8, 8, 300, 64), (12, 14, 2, 300, 64), (2, 14, 2, 300, 128), (8, 2, 8, 520, 256)]
 
 
-@pytest.mark.parametrize("wtype,output_type,embd_type,n_ctx", CASES)
-def test_decode_step_equals_composed_ops(gpu, wtype, output_type, embd_type, n_ctx):
+@pytest.mark.parametrize("wtype,output_type,embd_type,n_ctx,head_dim", CASES)
+def test_decode_step_equals_composed_ops(gpu, wtype, output_type, embd_type, n_ctx, head_dim):
     """Every driver step is bit-identical (logits, chosen token, KV caches, state) to the same step composed from
     the separately tested entry points: the driver adds only wiring, and the wiring is exact."""
     import torch
 
     from p100_amd import llama
 
-    model = tiny_model(wtype, output_type, n_ctx, embd_type=embd_type)
+    model = tiny_model(wtype, output_type, n_ctx, embd_type=embd_type, head_dim=head_dim)
     dec = llama.Decoder(model, max_prompt=8)
     prompt = [3, 999, 0, 512, 77, 77, 250, 1]
     dec.reset(prompt)
@@ -383,8 +386,8 @@ def test_decode_step_equals_composed_ops(gpu, wtype, output_type, embd_type, n_c
             toks.append(want_tok)
 
 
-@pytest.mark.parametrize("wtype,output_type,embd_type,n_ctx", CASES)
-def test_decode_step_matches_reference(orc, gpu, wtype, output_type, embd_type, n_ctx):
+@pytest.mark.parametrize("wtype,output_type,embd_type,n_ctx,head_dim", CASES)
+def test_decode_step_matches_reference(orc, gpu, wtype, output_type, embd_type, n_ctx, head_dim):
     """Each position's logits against the CPU restatement fed the same token and the GPU's own cache history.
 
     The two sides round differently in the last fp32 bit; where such a difference straddles a Q8_1 rounding
@@ -393,7 +396,7 @@ def test_decode_step_matches_reference(orc, gpu, wtype, output_type, embd_type, 
     position within 5e-2, and the greedy choice equal to the reference's wherever its margin exceeds that."""
     from p100_amd import llama
 
-    model = tiny_model(wtype, output_type, n_ctx, embd_type=embd_type)
+    model = tiny_model(wtype, output_type, n_ctx, embd_type=embd_type, head_dim=head_dim)
     dec = llama.Decoder(model, max_prompt=8)
     ref = RefLlama(orc, model)
     prompt = [3, 999, 0, 512, 77, 77, 250, 1]
