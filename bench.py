@@ -309,7 +309,7 @@ def extra_measurements(torch, P, lib, synth, timer, gen, layers, xs, ctxs):
             nsets = max(2, min(8, (600 << 20) // (M * K)))
             wsets = [synth.random_weights(wtype, M, K, generator=gen) for _ in range(nsets)]
             rb = P.row_bytes(wtype, K)
-            for n in (1, 2, 4, 8):
+            for n in (1, 2, 4, 8, 16):  # 16: the int8 matrix-core form (9..16 columns)
                 x = torch.randn((n, K), device=dev, generator=gen)
                 y = torch.empty((n, M), device=dev)
                 wsz = lib.p1x_mul_mat_vec_workspace(wtype, M, K, n, 0)

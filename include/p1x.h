@@ -20,7 +20,8 @@
  *                            bench/micro/h2_mmv.cu:99-113
  *   p1x_mul_mat_vec          ggml_cuda_mul_mat_vec_q (0005 patch hook :402-410) with the MMVH branch
  *                            ggml_cuda_should_use_mmvh / ggml_cuda_mul_mat_vec_h (0005 patch :344-377)
- *   p1x_mul_mat_vec_q8_1     mul_mat_vec_q with an already quantized src1 (mmvq.cu:318)
+ *   p1x_mul_mat_vec_q8_1     mul_mat_vec_q with an already quantized src1 (mmvq.cu:318); 9..16 columns take the
+ *                            place of ggml's mul_mat_q for small batches (docs/research/volta-fa-p9-lessons-2026-10-11.md:23-42)
  *   p1x_mul_mat_vec_h16      mmvh_mat_vec launch (0005 patch :277-340, 0006 patch :110-206)
  *   p1x_attn_validate        p100::validate (include/p100/attention.h:43, src/reference/attention_reference.cpp:18-32)
  *   p1x_flash_attn_decode    ggml_cuda_flash_attn_ext for n_q small with f16 K/V (fattn.cu:541-719 selection;
@@ -82,7 +83,8 @@ int p1x_quantize_q8_1(const float* x, int8_t* qs, float* ds, int64_t K, int64_t 
 int p1x_prepare_h16(const float* x, uint16_t* h, float* meta, int64_t K, int64_t ncols, void* stream);
 
 /*
- * y[c*M + m] = sum_k deq(w[m])[k] * x[c*K + k] for c < ncols (1..8), m < M.
+ * y[c*M + m] = sum_k deq(w[m])[k] * x[c*K + k] for c < ncols, m < M. ncols (ne11) is 1..8, and 1..16 for q4_0 /
+ * q8_0 with P1X_ACT_Q8_1 (9..16 columns run on int8 matrix cores; the int32 block sums are the same).
  *   w          M rows of GGUF blocks, row stride nb01 bytes (>= K/blk*blk_bytes, even); w 4-byte aligned.
  *   x          f32 [ncols][K]; K a multiple of the type's block size (32, or 256 for q4_K / q6_K).
  *   group_sums optional (NULL to skip; P1X_ACT_Q8_1 only): int32 [ncols][M][K/G], G = 16 for q6_K else 32,

@@ -20,7 +20,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # gfx950 only; packed FP32 instructions disabled (they are not used by these kernels on purpose).
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-I", str(PKG.parent / "include")]
-SOURCES = ["act.hip", "mmvq.hip", "mmvh.hip", "fattn.hip", "glue.hip", "capi.cpp", "decode.cpp"]
+SOURCES = ["act.hip", "mmvq.hip", "mmq.hip", "mmvh.hip", "fattn.hip", "glue.hip", "capi.cpp", "decode.cpp"]
 
 
 def _compile(src: str) -> pathlib.Path:

@@ -73,12 +73,15 @@ size_t h16_bytes(int64_t K, int64_t ncols) { return align256(size_t(K) * ncols *
 
 bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0; }
 
-int check_matvec(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K, int64_t ncols, const float* y) {
+int check_matvec(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K, int64_t ncols, const float* y,
+                 int max_cols) {
     if (block_bytes(wtype) == 0) return fail(P1X_EUNSUPPORTED, "unsupported weight type " + std::to_string(wtype));
     if (!w || !y) return fail(P1X_EINVAL, "null weight or output pointer");
     if (M <= 0 || K <= 0 || M > INT32_MAX || K > INT32_MAX) return fail(P1X_EINVAL, "M and K must be in 1..INT_MAX");
     if (K % block_elems(wtype)) return fail(P1X_EINVAL, "K must be a multiple of the block size");
-    if (ncols < 1 || ncols > 8) return fail(P1X_EINVAL, "ncols (ne11) must be 1..8");
+    if (ncols < 1 || ncols > max_cols)
+        return fail(P1X_EINVAL, max_cols == 8 ? "ncols (ne11) must be 1..8 (up to 16 for q4_0 / q8_0 with a Q8_1 activation)"
+                                              : "ncols (ne11) must be 1..16");
     if (nb01 < K / block_elems(wtype) * block_bytes(wtype)) return fail(P1X_EINVAL, "row stride nb01 shorter than a row");
     if (nb01 % 2) return fail(P1X_EINVAL, "row stride nb01 must be even (GGUF blocks are 2-byte aligned)");
     if ((wtype == P1X_Q4_K) && nb01 % 4) return fail(P1X_EINVAL, "q4_K row stride must be a multiple of 4");
@@ -192,27 +195,32 @@ int p1x_prepare_h16(const float* x, uint16_t* h, float* meta, int64_t K, int64_t
 }
 
 size_t p1x_mul_mat_vec_workspace(int wtype, int64_t M, int64_t K, int64_t ncols, int act_mode) {
-    (void)wtype;
     if (K <= 0 || ncols <= 0 || M <= 0) return 0;
     if (act_mode == P1X_ACT_H16) return h16_bytes(K, ncols);
-    return K <= INT32_MAX && M <= INT32_MAX && p1x::mmvq_fused_fits(int(ncols), int(M), int(K)) ? 0 : q8_1_bytes(K, ncols);
+    const bool fused = ncols <= 8 && K <= INT32_MAX && M <= INT32_MAX && !p1x::mmq_preferred(wtype, int(ncols)) &&
+                       p1x::mmvq_fused_fits(int(ncols), int(M), int(K));
+    return fused ? 0 : q8_1_bytes(K, ncols);
 }
 
 int p1x_mul_mat_vec_q8_1(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K, const int8_t* qs,
                          const float* ds, int64_t ncols, float* y, int32_t* group_sums, void* stream) {
     if (int rc = ensure_init()) return rc;
-    if (int rc = check_matvec(wtype, w, nb01, M, K, ncols, y)) return rc;
+    if (int rc = check_matvec(wtype, w, nb01, M, K, ncols, y, p1x::mmq_supported(wtype, 16) ? 16 : 8)) return rc;
     if (!qs || !ds) return fail(P1X_EINVAL, "null activation pointer");
     if (!aligned(qs, 16) || !aligned(ds, 16)) return fail(P1X_EINVAL, "qs and ds must be 16-byte aligned");
-    hipError_t e = p1x::launch_mmvq(wtype, int(ncols), w, nb01, int(M), int(K), qs, ds, nullptr, y, group_sums,
-                                    static_cast<hipStream_t>(stream));
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (ncols > 8 && !p1x::mmq_fits(int(M), nb01, int(K), int(ncols)))
+        return fail(P1X_EUNSUPPORTED, "9..16 columns need the weights (M * nb01) within 2 GiB");
+    hipError_t e = p1x::mmq_preferred(wtype, int(ncols)) && p1x::mmq_fits(int(M), nb01, int(K), int(ncols))
+                       ? p1x::launch_mmq(wtype, int(ncols), w, nb01, int(M), int(K), qs, ds, y, group_sums, s)
+                       : p1x::launch_mmvq(wtype, int(ncols), w, nb01, int(M), int(K), qs, ds, nullptr, y, group_sums, s);
     return e == hipSuccess ? P1X_OK : hip_fail(e, "mul_mat_vec_q8_1");
 }
 
 int p1x_mul_mat_vec_h16(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K, const uint16_t* h,
                         const float* meta, int64_t ncols, float* y, void* stream) {
     if (int rc = ensure_init()) return rc;
-    if (int rc = check_matvec(wtype, w, nb01, M, K, ncols, y)) return rc;
+    if (int rc = check_matvec(wtype, w, nb01, M, K, ncols, y, 8)) return rc;
     if (!h || !meta) return fail(P1X_EINVAL, "null activation pointer");
     if (!aligned(h, 16) || !aligned(meta, 8)) return fail(P1X_EINVAL, "h must be 16-byte and meta 8-byte aligned");
     hipError_t e = p1x::launch_mmvh(wtype, int(ncols), w, nb01, int(M), int(K), h, meta, y,
@@ -223,7 +231,9 @@ int p1x_mul_mat_vec_h16(int wtype, const void* w, int64_t nb01, int64_t M, int64
 int p1x_mul_mat_vec(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K, int act_mode, const float* x,
                     int64_t ncols, float* y, int32_t* group_sums, void* ws, size_t ws_bytes, void* stream) {
     if (int rc = ensure_init()) return rc;
-    if (int rc = check_matvec(wtype, w, nb01, M, K, ncols, y)) return rc;
+    if (int rc = check_matvec(wtype, w, nb01, M, K, ncols, y,
+                              act_mode == P1X_ACT_Q8_1 && p1x::mmq_supported(wtype, 16) ? 16 : 8))
+        return rc;
     if (!x) return fail(P1X_EINVAL, "null activation pointer");
     if (act_mode != P1X_ACT_Q8_1 && act_mode != P1X_ACT_H16) return fail(P1X_EINVAL, "unknown activation mode");
     if (act_mode == P1X_ACT_H16 && group_sums)
@@ -243,9 +253,13 @@ int p1x_mul_mat_vec(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K
     if (act_mode == P1X_ACT_Q8_1) {
         auto* qs = reinterpret_cast<int8_t*>(base);
         auto* ds = reinterpret_cast<float*>(base + align256(size_t(K) * ncols));
+        if (ncols > 8 && !p1x::mmq_fits(int(M), nb01, int(K), int(ncols)))
+            return fail(P1X_EUNSUPPORTED, "9..16 columns need the weights (M * nb01) within 2 GiB");
         hipError_t e = p1x::launch_quantize_q8_1(x, qs, ds, int(K), int(ncols), s);
         if (e != hipSuccess) return hip_fail(e, "quantize_q8_1");
-        e = p1x::launch_mmvq(wtype, int(ncols), w, nb01, int(M), int(K), qs, ds, nullptr, y, group_sums, s);
+        e = p1x::mmq_preferred(wtype, int(ncols)) && p1x::mmq_fits(int(M), nb01, int(K), int(ncols))
+                ? p1x::launch_mmq(wtype, int(ncols), w, nb01, int(M), int(K), qs, ds, y, group_sums, s)
+                : p1x::launch_mmvq(wtype, int(ncols), w, nb01, int(M), int(K), qs, ds, nullptr, y, group_sums, s);
         return e == hipSuccess ? P1X_OK : hip_fail(e, "mul_mat_vec_q8_1");
     }
     auto* h = reinterpret_cast<uint16_t*>(base);

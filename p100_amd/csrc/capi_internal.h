@@ -22,7 +22,8 @@ int block_bytes(int wtype);
 size_t align256(size_t n);
 size_t q8_1_bytes(int64_t K, int64_t ncols);
 bool aligned(const void* p, size_t n);
-int check_matvec(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K, int64_t ncols, const float* y);
+int check_matvec(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K, int64_t ncols, const float* y,
+                 int max_cols);
 
 // Attention argument checks and kernel arguments shared by the attention entry points and the decode driver.
 size_t fa_workspace(const p1x_attn_params* p);

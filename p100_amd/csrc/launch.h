@@ -14,6 +14,14 @@ hipError_t launch_round_fp16(const float* x, uint16_t* out, int64_t n, hipStream
 hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
                        const float* x, float* y, int32_t* gs, hipStream_t stream);
 bool mmvq_fused_fits(int B, int M, int K);
+// Several activation columns on int8 matrix cores (mmq.hip): q4_0 / q8_0 weights, 1..kMmqMaxCols columns of a
+// prepared Q8_1 activation.
+constexpr int kMmqMaxCols = 16;
+bool mmq_supported(int type, int B);
+bool mmq_preferred(int type, int B);  // the form chosen for B columns (always for B > 8)
+bool mmq_fits(int M, int64_t nb01, int K, int B);  // weight and activation byte ranges within 32-bit buffer offsets
+hipError_t launch_mmq(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
+                      float* y, int32_t* gs, hipStream_t stream);
 hipError_t launch_mmvh(int type, int B, const void* w, int64_t nb01, int M, int K, const uint16_t* h,
                        const float* meta, float* y, hipStream_t stream);
 

@@ -1,0 +1,250 @@
+// Quantized mat-vec for several activation columns (ne11 up to 16) on int8 matrix cores.
+//
+// The product of a 32-element weight block with a 32-element Q8_1 activation block is one K step of
+// v_mfma_i32_16x16x32_i8, so one instruction yields the exact int32 block sums of 16 weight rows x 16 columns
+// (the reference's per-block integer dot products, bit for bit); each block's sums are then scaled in FP32 with
+// the same per-block formula as the dot4 path (src/reference/qmv_model.cpp q81 path: q4_0 d*(dot*d8 - 8*s8),
+// q8_0 d*d8*dot). Where the dot4 path re-reads every activation column for every weight row, here one wave
+// serves 16 rows per activation read, which is what makes 4..16 columns cheap.
+//
+// Lane layout of v_mfma_i32_16x16x32_i8 (checked on the device): A (16 x 32) lane l holds row l % 16, elements
+// 8 (l / 16) .. + 7; B (32 x 16) lane l holds column l % 16, the same elements; D (16 x 16) lane l holds rows
+// 4 (l / 16) .. + 3 of column l % 16. A = weights, B = activation, so a lane's four results share its own
+// activation column (one scale load) and need the weight scales of four rows (four ds_bpermute).
+//
+// Work-group: 16 weight rows, P1X_MMQ_WAVES waves, each over a contiguous share of the K blocks, P1X_MMQ_UNROLL
+// blocks per step with the next step's loads in flight; the partial 16 x 16 tiles are added in LDS in a fixed
+// order (deterministic, no workspace). Grid: ceil(M / 16).
+#include "common.h"
+#include "launch.h"
+
+namespace p1x {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// Per weight type: block bytes and the per-block FP32 scaling of the integer block sum (the dot4 path's
+// arithmetic, so both forms round alike; only the order of the block sums differs).
+template <int TYPE>
+struct MfmaW;
+
+// q4_0: 18-byte block {fp16 d, qs[16]}; element e < 16 is the low nibble of qs[e], e + 16 the high nibble, taken
+// unsigned (0..15) as the reference's q81 path does: acc + d * (dot * d8 - 8 * s8) (UnitQ4_0::acc).
+template <>
+struct MfmaW<Q4_0> {
+    static constexpr int kBytes = 18;
+    static __device__ __forceinline__ float acc(float dw, int dot, float4 xs, float a) {
+        return fmaf(dw, fmaf(float(dot), xs.x, -8.0f * xs.y), a);
+    }
+};
+
+// q8_0: 34-byte block {fp16 d, int8 qs[32]}: acc + (d * d8) * dot (UnitQ8_0::acc).
+template <>
+struct MfmaW<Q8_0> {
+    static constexpr int kBytes = 34;
+    static __device__ __forceinline__ float acc(float dw, int dot, float4 xs, float a) {
+        return fmaf(dw * xs.x, float(dot), a);
+    }
+};
+
+#ifndef P1X_MMQ_PAD
+#define P1X_MMQ_PAD 4
+#endif
+constexpr int kMmqWaves = 4;    // waves per work-group, each over a contiguous quarter of the K blocks
+constexpr int kStepBlocks = 8;  // K blocks per step (staged through LDS)
+
+// Buffer loads with a range check: offsets at or past the resource size read zeros and touch no memory, so the
+// staging loads past the matrix end, past the last activation column or in padded columns need no branch.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+constexpr uint32_t kOob = 0x7ffffff0u;
+
+// Per-wave LDS staging area of one step: the 16 weight rows' bytes of 8 blocks (dword-aligned spans, 4 lanes x NWL
+// 16-byte loads per row: 192 bytes for q4_0, 320 for q8_0, each covering 8 blocks plus the 2-byte alignment shift),
+// the 16 activation columns' 8 blocks as [block][column][32 bytes] (the MFMA B-operand reads are then 512
+// contiguous bytes per block), and their Q8_1 scales [block][column].
+template <int ROWDW>
+struct MmqStage {
+    uint32_t w[16][ROWDW];
+    uint32_t a[kStepBlocks][16][8];
+    float4 s[kStepBlocks][16];
+};
+
+template <int TYPE, bool SUMS>
+__global__ __launch_bounds__(64 * kMmqWaves) void k_mmq_mfma(const uint8_t* __restrict__ w, int64_t nb01, int M, int K,
+                                                            int B, const int8_t* __restrict__ xq,
+                                                            const float4* __restrict__ xds, float* __restrict__ y,
+                                                            int32_t* __restrict__ gs) {
+    using W = MfmaW<TYPE>;
+    constexpr int U = kStepBlocks;
+    constexpr int BB = W::kBytes;
+    constexpr int NWL = (U * BB + 4 + 63) / 64;  // 16-byte loads per lane (4 lanes per row)
+    constexpr int ROWDW = 16 * NWL + P1X_MMQ_PAD;  // staged dwords per row (padding spreads rows over LDS banks)
+    __shared__ MmqStage<ROWDW> stage[kMmqWaves];
+    __shared__ float red[kMmqWaves - 1][4][64];  // partial tiles of waves 1.., result-major (conflict-free)
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, i16 = lane & 15;
+    const int m0 = blockIdx.x * 16;
+    const int nblk = K / 32;
+    const int per = (nblk + kMmqWaves - 1) / kMmqWaves;
+    const int b0 = min(nblk, wave * per), b1 = min(nblk, b0 + per);
+    MmqStage<ROWDW>& st = stage[wave];
+
+    // Global side of the staging: lane (row lane/4, quarter lane%4) reads NWL x 16 bytes of its row's dword-aligned
+    // span.
+    const auto wr = rsrc(w, uint32_t(size_t(M) * nb01));
+    const int srow = lane >> 2, sq = lane & 3;
+    const uint32_t srow_off = uint32_t(size_t(min(m0 + srow, M - 1)) * nb01);
+    const auto xr = rsrc(xq, uint32_t(size_t(B) * K));          // columns past B read zeros
+    const auto dr = rsrc(xds, uint32_t(size_t(B) * nblk * 16));
+    // MFMA side: the lane's A-operand row (i16) and the rows 4g..4g+3 whose scales it applies; byte 0 of each
+    // row's staged span is the dword holding the row's first byte of the step.
+    auto row_shift = [&](int row, int bs) { return int((size_t(min(m0 + row, M - 1)) * nb01 + size_t(bs) * BB) & 3); };
+    uint4 rw[NWL], ra[4], rs[2];
+    auto load = [&](int bs) {
+        const uint32_t wb = (srow_off + uint32_t(bs) * BB) & ~3u;
+#pragma unroll
+        for (int k = 0; k < NWL; ++k) rw[k] = ld16(wr, wb + (sq * NWL + k) * 16);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {  // piece p: column p / 16, 16-byte piece p % 16 of the column's 256 bytes
+            const int p = j * 64 + lane, c = p >> 4;
+            ra[j] = ld16(xr, c < B ? uint32_t(c * K + bs * 32 + (p & 15) * 16) : kOob);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {  // piece p: column p / 8, block p % 8
+            const int p = j * 64 + lane, c = p >> 3;
+            rs[j] = ld16(dr, c < B ? uint32_t((c * nblk + bs + (p & 7)) * 16) : kOob);
+        }
+    };
+    auto store = [&]() {
+#pragma unroll
+        for (int k = 0; k < NWL; ++k) *reinterpret_cast<uint4*>(&st.w[srow][(sq * NWL + k) * 4]) = rw[k];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int p = j * 64 + lane, c = p >> 4, k16 = p & 15;
+            *reinterpret_cast<uint4*>(&st.a[k16 >> 1][c][(k16 & 1) * 4]) = ra[j];
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int p = j * 64 + lane;
+            st.s[p & 7][p >> 3] = __builtin_bit_cast(float4, rs[j]);
+        }
+    };
+    // 16-bit field at byte offset o of staged row r.
+    auto u16_at = [&](int r, int o) { return (st.w[r][o >> 2] >> (8 * (o & 2))) & 0xffffu; };
+    // 4*N bytes at byte offset o (2-byte aligned) of staged row r, as dwords.
+    auto bytes_at = [&](int r, int o, uint32_t* out, int n) {
+        const int d0 = o >> 2;
+        const uint32_t sel = (o & 2) ? 0x05040302u : 0x03020100u;
+        for (int k = 0; k < n; ++k) out[k] = perm(st.w[r][d0 + k + 1], st.w[r][d0 + k], sel);
+    };
+
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (b0 < b1) {
+        load(b0);
+        for (int bs = b0; bs < b1; bs += U) {
+            // The wave's own LDS area: the previous step's reads complete before these writes, and these writes
+            // before this step's reads (other lanes of the wave read them).
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            store();
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            load(bs + U);  // the next step's loads are in flight while this one computes (past b1: never used)
+            const int sh = row_shift(i16, bs);
+            int shr[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) shr[r] = row_shift(4 * g + r, bs);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const bool ok = bs + u < b1;
+                // A operand: 8 weight elements 8g..8g+7 of block u of row i16.
+                long wa;
+                if constexpr (TYPE == Q4_0) {
+                    uint32_t q2[2];
+                    bytes_at(i16, sh + u * BB + 2 + 8 * (g & 1), q2, 2);
+                    const uint32_t shn = (g & 2) ? 4u : 0u;
+                    wa = long((q2[0] >> shn) & 0x0F0F0F0Fu) | (long((q2[1] >> shn) & 0x0F0F0F0Fu) << 32);
+                } else {
+                    uint32_t q2[2];
+                    bytes_at(i16, sh + u * BB + 2 + 8 * g, q2, 2);
+                    wa = long(q2[0]) | (long(q2[1]) << 32);
+                }
+                const long xa = *reinterpret_cast<const long*>(&st.a[u][i16][2 * g]);
+                const float4 xs = st.s[u][i16];
+                const v4i zero = {0, 0, 0, 0};
+                const v4i dd = __builtin_amdgcn_mfma_i32_16x16x32_i8(wa, xa, zero, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float dw = half_bits_to_float(u16_at(4 * g + r, shr[r] + u * BB));
+                    const float v = W::acc(dw, dd[r], xs, acc[r]);
+                    acc[r] = ok ? v : acc[r];
+                    if (SUMS) {
+                        const int m = m0 + 4 * g + r;
+                        if (ok && i16 < B && m < M) gs[(size_t(i16) * M + m) * nblk + bs + u] = dd[r];
+                    }
+                }
+            }
+        }
+    }
+
+    // Waves 1.. hand their partial tiles to wave 0, which adds them in wave order and stores.
+    if (wave > 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave - 1][r][lane] = acc[r];
+    }
+    __syncthreads();
+    if (wave != 0 || i16 >= B) return;
+#pragma unroll
+    for (int k = 0; k < kMmqWaves - 1; ++k)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] += red[k][r][lane];
+    const int mrow = m0 + 4 * g;
+    float* dst = y + size_t(i16) * M + mrow;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        if (mrow + r < M) dst[r] = acc[r];
+}
+
+}  // namespace
+
+#ifndef P1X_MMQ_MIN_COLS
+#define P1X_MMQ_MIN_COLS 9  // columns from which the matrix-core form replaces the dot4 kernels
+#endif
+
+bool mmq_supported(int type, int B) { return (type == Q4_0 || type == Q8_0) && B >= 1 && B <= kMmqMaxCols; }
+// The staging loads address the weight matrix through one 32-bit buffer range.
+bool mmq_fits(int M, int64_t nb01, int K, int B) {
+    return int64_t(M) * nb01 <= int64_t(kOob) && int64_t(B) * K <= int64_t(kOob) &&
+           int64_t(B) * (K / 32) * 16 <= int64_t(kOob);
+}
+bool mmq_preferred(int type, int B) { return mmq_supported(type, B) && B >= P1X_MMQ_MIN_COLS; }
+
+hipError_t launch_mmq(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
+                      float* y, int32_t* gs, hipStream_t stream) {
+    const dim3 grid((M + 15) / 16);
+    const auto* wb = static_cast<const uint8_t*>(w);
+    const auto* d4 = reinterpret_cast<const float4*>(xds);
+#define P1X_MMQ(T, S) \
+    hipLaunchKernelGGL((k_mmq_mfma<T, S>), grid, dim3(64 * kMmqWaves), 0, stream, wb, nb01, M, K, B, xq, d4, y, gs)
+    if (type == Q4_0) {
+        if (gs) P1X_MMQ(Q4_0, true);
+        else P1X_MMQ(Q4_0, false);
+    } else if (type == Q8_0) {
+        if (gs) P1X_MMQ(Q8_0, true);
+        else P1X_MMQ(Q8_0, false);
+    } else {
+        return hipErrorInvalidValue;
+    }
+#undef P1X_MMQ
+    return hipGetLastError();
+}
+
+}  // namespace p1x

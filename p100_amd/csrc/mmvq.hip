@@ -25,6 +25,9 @@
 #ifndef P1X_MMVQ_MIN_WAVES_FX
 #define P1X_MMVQ_MIN_WAVES_FX 2048  // the same for the single-launch form (fewer work-groups: less requantizing)
 #endif
+#ifndef P1X_MMVQ_MIN_WAVES_MB
+#define P1X_MMVQ_MIN_WAVES_MB 4096  // the same for several activation columns (rows per wave amortise their reads)
+#endif
 #ifndef P1X_MMVQ_FUSE_MAX
 #define P1X_MMVQ_FUSE_MAX (1L << 21)  // single launch while work-groups x B x K stays at or below this
 #endif
@@ -490,8 +493,8 @@ hipError_t launch_type(int B, const uint8_t* w, int64_t nb01, int M, int K, int 
 
 // Rows per wave: the most (up to 4) that still leaves enough waves to fill the 256 CUs (4096 for the kernel on a
 // prepared activation, 2048 for the single-launch form, which requantizes x once per work-group).
-int mmvq_rows_per_wave(int M, bool fused) {
-    const int min_waves = fused ? P1X_MMVQ_MIN_WAVES_FX : P1X_MMVQ_MIN_WAVES;
+int mmvq_rows_per_wave(int M, int B, bool fused) {
+    const int min_waves = fused ? P1X_MMVQ_MIN_WAVES_FX : (B > 1 ? P1X_MMVQ_MIN_WAVES_MB : P1X_MMVQ_MIN_WAVES);
     for (int rw : {4, 2})
         if (rw <= P1X_MMVQ_MAX_RW && M / rw >= min_waves) return rw;
     return 1;
@@ -501,14 +504,14 @@ int mmvq_rows_per_wave(int M, bool fused) {
 // 64 KiB of LDS and the repeated quantization (work-groups x B x K elements) stays small next to the weight
 // stream; otherwise the activation goes through p1x_quantize_q8_1 and a workspace.
 bool mmvq_fused_fits(int B, int M, int K) {
-    const int rw = mmvq_rows_per_wave(M, true);
+    const int rw = mmvq_rows_per_wave(M, B, true);
     const long wgs = (M + 4L * rw - 1) / (4L * rw);  // every work-group quantizes all B x K elements
     return size_t(48) * B * (K / 32) <= 65536 && wgs * K * B <= P1X_MMVQ_FUSE_MAX;
 }
 
 hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
                        const float* x, float* y, int32_t* gs, hipStream_t stream) {
-    const int rw = mmvq_rows_per_wave(M, x != nullptr);
+    const int rw = mmvq_rows_per_wave(M, B, x != nullptr);
     const auto* wb = static_cast<const uint8_t*>(w);
     const auto* d4 = reinterpret_cast<const float4*>(xds);
     switch (type) {

@@ -155,6 +155,24 @@ def test_mmvq_parity(orc, gpu, tname):
     print(f"{tname} q81 worst |y-exact|/(|w||x|) = {worst:.3e}")
 
 
+@pytest.mark.parametrize("tname", ["q4_0", "q8_0"])
+def test_many_columns_parity(orc, gpu, tname):
+    """9..16 activation columns (the int8 matrix-core form): int32 group sums bit-exact, FP32 within the bars;
+    K of one and two blocks (idle waves in the K split), partial 16-row tiles, and a full-size shape."""
+    import p100_amd as P
+
+    t = orc.TYPES[tname]
+    for k, rows in ((32, 17), (64, 33), (96, 16), (4096, 17), (14336, 33), (4096, 4096)):
+        for ncols in ((9, 12, 16) if rows < 4096 else (16,)):
+            w, x = make_case(orc, t, k, rows, ncols, seed=900 + k + rows + ncols)
+            y, sums = P.mul_mat_vec(t, to_dev(w), rows, k, to_dev(x), act="q8_1", group_sums=True)
+            check_matvec(orc, t, w, x, y.cpu().numpy(), sums.cpu().numpy(), "q81")
+            y2 = P.mul_mat_vec(t, to_dev(w), rows, k, to_dev(x), act="q8_1").cpu().numpy()
+            y3 = P.mul_mat_vec(t, to_dev(w), rows, k, P.quantize_q8_1(to_dev(x))).cpu().numpy()
+            assert (y2.view(np.uint32) == y.cpu().numpy().view(np.uint32)).all()
+            assert (y3.view(np.uint32) == y2.view(np.uint32)).all()
+
+
 @pytest.mark.parametrize("tname", TYPES)
 @pytest.mark.parametrize("scale", [1e5, 1e-5])
 def test_mmvq_activation_ranges(orc, gpu, tname, scale):
@@ -224,7 +242,9 @@ def test_invalid_arguments(gpu):
     with pytest.raises(ValueError, match="multiple of the block size"):
         P.mul_mat_vec("q4_K", w, 1, 32, x)
     with pytest.raises(ValueError, match="ncols"):
-        P.mul_mat_vec("q4_0", w, 1, 32, torch.zeros((9, 32), device="cuda"))
+        P.mul_mat_vec("q4_0", w, 1, 32, torch.zeros((17, 32), device="cuda"))
+    with pytest.raises(ValueError, match="ncols"):  # 9..16 columns: q4_0 / q8_0 with a Q8_1 activation only
+        P.mul_mat_vec("q4_0", w, 1, 32, torch.zeros((9, 32), device="cuda"), act="h16")
     with pytest.raises(ValueError, match="row stride"):
         P.mul_mat_vec("q4_0", w, 1, 32, x, nb01=16)
     with pytest.raises(P.P1XError):
