@@ -130,7 +130,10 @@ def main():
         print(json.dumps({"only": "roofline", "roofline": roof, "calibration_copy_bytes": 32 << 20}))
         return
     if args.only == "fa":
-        print(json.dumps({"only": "fa", "fa_decode": measure_fa(torch, P, lib, timer, gen, args.fa_ctx)}))
+        rec = {"only": "fa", "fa_decode": measure_fa(torch, P, lib, timer, gen, args.fa_ctx)}
+        for kv_type in ("q8_0", "q4_0"):
+            rec[f"fa_decode_{kv_type}_kv"] = measure_fa_quant(torch, P, lib, synth, timer, gen, args.fa_ctx, kv_type)
+        print(json.dumps(rec))
         return
 
     def op(wt, M, K, x, y, s):
@@ -265,6 +268,37 @@ def measure_fa(torch, P, lib, timer, gen, ctxs):
                       "+ LSE combine pass (2 launches, timed together)", "by_ctx": fa}
 
 
+def measure_fa_quant(torch, P, lib, synth, timer, gen, ctxs, kv_type):
+    """FA decode over a q8_0 / q4_0 KV cache (in-kernel dequantization), same shape as measure_fa."""
+    dev = torch.device("cuda")
+    t = P.TYPES[kv_type]
+    row = 128 // 32 * P.BLOCK[t][1]
+    fa = {}
+    for ctx in ctxs:
+        p = P.AttnParams(n_head_q=32, n_head_kv=8, seq_q=1, seq_kv=ctx, d_qk=128, d_v=128, causal=True)
+        nsets = max(2, min(16, (600 << 20) // (2 * 8 * ctx * row)))
+        caches = [(synth.random_weights(t, 8 * ctx, 128, std=1.0, generator=gen),
+                   synth.random_weights(t, 8 * ctx, 128, std=1.0, generator=gen)) for _ in range(nsets)]
+        q = torch.randn(32 * 128, device=dev, generator=gen)
+        o = torch.empty(32 * 128, device=dev)
+        lse = torch.empty(32, device=dev)
+        fws = torch.empty(P.flash_attn_decode_workspace(p) // 4 + 4, device=dev)
+
+        def call(i, s, p=p, caches=caches, q=q, o=o, lse=lse, fws=fws):
+            k, v = caches[i % len(caches)]
+            lib.p1x_flash_attn_decode_quant(C.byref(p), t, C.c_void_p(q.data_ptr()), C.c_void_p(k.data_ptr()),
+                                            C.c_void_p(v.data_ptr()), None, None, None, C.c_void_p(o.data_ptr()),
+                                            C.c_void_p(lse.data_ptr()), C.c_void_p(fws.data_ptr()), fws.numel() * 4, s)
+
+        med, mn, _ = timer.period_us(call, n=32)
+        b = 2 * 8 * ctx * row + 32 * 128 * 4 * 2  # quantized K and V once per KV head, q and o in f32
+        fa[str(ctx)] = {"us": round(med, 3), "min_us": round(mn, 3), "bytes": b,
+                        "gbs": round(b / (med * 1e-6) / 1e9, 1), "frac": round(b / (med * 1e-6) / 1e9 / PEAK_GBS, 4)}
+        log(f"[bench] FA decode {kv_type} KV ctx {ctx}: {med:.2f} us ({fa[str(ctx)]['gbs']} GB/s)")
+        del caches
+    return {"config": f"as fa_decode with a {kv_type} KV cache dequantized in-kernel", "by_ctx": fa}
+
+
 def extra_measurements(torch, P, lib, synth, timer, gen, layers, xs, ctxs):
     dev = torch.device("cuda")
     out = {}
@@ -329,6 +363,8 @@ def extra_measurements(torch, P, lib, synth, timer, gen, layers, xs, ctxs):
 
     out["fa_decode"] = measure_fa(torch, P, lib, timer, gen, sorted(set(ctxs) | {640}))
     fa = out["fa_decode"]["by_ctx"]
+    for kv_type in ("q8_0", "q4_0"):
+        out[f"fa_decode_{kv_type}_kv"] = measure_fa_quant(torch, P, lib, synth, timer, gen, (2048, 8192, 32768), kv_type)
 
     # 8B-shape decode tokens/s from measured periods: 32 x (layer step with shared Q8_1 + FA decode @ctx 640)
     # + Q4_0 output projection 128256x4096. Norm/RoPE/SwiGLU/KV-append glue kernels are not included.

@@ -29,6 +29,8 @@
  *                            p100::attention_reference (include/p100/attention.h:48-49)
  *   p1x_flash_attn_decode_kvlen  the same op over a KV-cache view whose valid length is known only on the device
  *                            (llama.cpp pads the view and masks the tail with the KQ mask; here the length is read)
+ *   p1x_flash_attn_decode_quant  the same op over a q8_0 / q4_0 KV cache, replacing the F16 conversion kernels that
+ *                            ggml runs first (third_party/patches/0001, 0002; bench/micro/dequant_nc.cu:1-14)
  * Decode-step glue and driver (the llama-bench decode runs, bench/phase0.sh:124, of the 8B shape modelled in
  * bin/decode-model.py:52-57; the ggml ops are restated from llama.cpp's Llama graph, not from this reference):
  *   p1x_get_rows             GGML_OP_GET_ROWS (token embedding), q4_0 / q8_0 rows
@@ -143,6 +145,17 @@ int p1x_flash_attn_decode(const p1x_attn_params* p, const float* q, const uint16
  */
 int p1x_flash_attn_decode_kvlen(const p1x_attn_params* p, const float* q, const uint16_t* k, const uint16_t* v,
                                 const p1x_kv_strides* strides, const float* mask, const int32_t* kv_len, float* o,
+                                float* lse, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Decode attention over a quantized KV cache (llama.cpp's -ctk / -ctv q8_0 or q4_0; kv_type P1X_Q8_0 or P1X_Q4_0
+ * for both K and V): each K / V row of d values is d/32 GGUF blocks, dequantized inside the kernel (d * q, exact
+ * in FP32) instead of a conversion pass to fp16. byte_strides (NULL = dense [batch][n_head_kv][seq_kv] rows) are
+ * in bytes and, with k / v, 4-byte aligned. kv_len optional as in p1x_flash_attn_decode_kvlen. Otherwise as
+ * p1x_flash_attn_decode (same workspace size).
+ */
+int p1x_flash_attn_decode_quant(const p1x_attn_params* p, int kv_type, const float* q, const void* k, const void* v,
+                                const p1x_kv_strides* byte_strides, const float* mask, const int32_t* kv_len, float* o,
                                 float* lse, void* ws, size_t ws_bytes, void* stream);
 
 /* fp32 -> IEEE binary16 bits with the device conversion the kernels use (round to nearest even). */

@@ -34,7 +34,8 @@ EXPORTS = ["p1x_version", "p1x_init", "p1x_last_error", "p1x_quantize_q8_1", "p1
            "p1x_mul_mat_vec_workspace", "p1x_mul_mat_vec", "p1x_mul_mat_vec_q8_1", "p1x_mul_mat_vec_h16",
            "p1x_attn_validate", "p1x_flash_attn_decode_workspace", "p1x_flash_attn_decode",
            "p1x_flash_attn_decode_kvlen", "p1x_round_to_fp16", "p1x_get_rows", "p1x_rms_norm_q8_1", "p1x_swiglu_q8_1",
-           "p1x_rope_kv_append", "p1x_argmax_workspace", "p1x_argmax", "p1x_llama_workspace", "p1x_llama_decode_step"]
+           "p1x_rope_kv_append", "p1x_argmax_workspace", "p1x_argmax", "p1x_llama_workspace", "p1x_llama_decode_step",
+           "p1x_flash_attn_decode_quant"]
 
 
 class P1XError(RuntimeError):
@@ -92,6 +93,8 @@ def load():
                                             vp, sz, vp]),
         "p1x_flash_attn_decode_kvlen": (C.c_int, [C.POINTER(AttnParams), vp, vp, vp, C.POINTER(KVStrides), vp, vp,
                                                   vp, vp, vp, sz, vp]),
+        "p1x_flash_attn_decode_quant": (C.c_int, [C.POINTER(AttnParams), C.c_int, vp, vp, vp, C.POINTER(KVStrides),
+                                                  vp, vp, vp, vp, vp, sz, vp]),
         "p1x_round_to_fp16": (C.c_int, [vp, vp, i64, vp]),
         "p1x_get_rows": (C.c_int, [C.c_int, vp, i64, i64, i64, vp, vp, vp]),
         "p1x_rms_norm_q8_1": (C.c_int, [vp, vp, vp, i64, C.c_float, vp, vp, vp, vp]),
@@ -284,6 +287,30 @@ def flash_attn_decode(p: AttnParams, q, k, v, mask=None, strides: KVStrides | No
     else:
         _check(lib.p1x_flash_attn_decode_kvlen(C.byref(p), _ptr(q), _ptr(k), _ptr(v), sp, _ptr(mask), _ptr(kv_len),
                                                _ptr(o), _ptr(l_out), _ptr(ws), nbytes, _stream(stream)))
+    return o, l_out
+
+
+def flash_attn_decode_quant(p: AttnParams, kv_type, q, k, v, mask=None, byte_strides: KVStrides | None = None,
+                            kv_len=None, want_lse=True, out=None, lse=None, workspace=None, stream=None):
+    """flash_attn_decode over a q8_0 / q4_0 KV cache: k, v uint8 tensors of GGUF blocks, rows of d_qk / 32 blocks
+    ([batch, n_head_kv, seq_kv] rows when dense; otherwise byte_strides)."""
+    import torch
+
+    lib = load()
+    p = _params(p)
+    why = validate(p)
+    if why:
+        raise ValueError(why)
+    dev = q.device
+    rows = p.batch * p.n_head_q * p.seq_q
+    o = out if out is not None else torch.empty(rows * p.d_v, dtype=torch.float32, device=dev)
+    l_out = (lse if lse is not None else torch.empty(rows, dtype=torch.float32, device=dev)) if want_lse else None
+    need = lib.p1x_flash_attn_decode_workspace(C.byref(p))
+    ws = workspace if workspace is not None else torch.empty(max(need, 16) // 4 + 4, dtype=torch.float32, device=dev)
+    sp = C.byref(byte_strides) if byte_strides is not None else None
+    _check(lib.p1x_flash_attn_decode_quant(C.byref(p), TYPES.get(kv_type, kv_type), _ptr(q), _ptr(k), _ptr(v), sp,
+                                           _ptr(mask), _ptr(kv_len), _ptr(o), _ptr(l_out), _ptr(ws),
+                                           ws.numel() * ws.element_size(), _stream(stream)))
     return o, l_out
 
 

@@ -108,7 +108,7 @@ size_t fa_workspace(const p1x_attn_params* p) {
 
 int fa_prepare(const p1x_attn_params* p, const float* q, const uint16_t* k, const uint16_t* v,
                const p1x_kv_strides* strides, const float* mask, const int32_t* kv_len, float* o, float* lse, void* ws,
-               size_t ws_bytes, FaArgs& a) {
+               size_t ws_bytes, FaArgs& a, bool kv_f16) {
     if (int rc = p1x_attn_validate(p)) return rc;
     if (!q || !k || !v || !o) return fail(P1X_EINVAL, "null q, k, v or o pointer");
     if (p->d_qk != p->d_v || (p->d_qk != 64 && p->d_qk != 128 && p->d_qk != 256))
@@ -116,7 +116,7 @@ int fa_prepare(const p1x_attn_params* p, const float* q, const uint16_t* k, cons
     const int64_t head_chunks = (p->n_head_q / p->n_head_kv) / fa_heads_per_wg(p->n_head_q, p->n_head_kv);
     if (p->seq_q > 65535 || int64_t(p->batch) * p->n_head_kv * head_chunks > 65535)
         return fail(P1X_EUNSUPPORTED, "seq_q and batch*n_head_kv*(query heads per KV head / heads per group) must be <= 65535");
-    if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16))
+    if (!aligned(q, 16) || (kv_f16 && (!aligned(k, 16) || !aligned(v, 16))))
         return fail(P1X_EINVAL, "q, k and v must be 16-byte aligned");
     const int64_t d = p->d_qk;
     a = FaArgs{};
@@ -125,7 +125,9 @@ int fa_prepare(const p1x_attn_params* p, const float* q, const uint16_t* k, cons
     a.v = reinterpret_cast<const __half*>(v);
     a.mask = mask;
     a.kv_len = kv_len;
-    if (strides) {
+    if (!kv_f16) {
+        // The caller sets the byte strides and spans of a quantized cache.
+    } else if (strides) {
         a.k_row = strides->k_row, a.k_head = strides->k_head, a.k_batch = strides->k_batch;
         a.v_row = strides->v_row, a.v_head = strides->v_head, a.v_batch = strides->v_batch;
         if (a.k_row % 8 || a.k_head % 8 || a.k_batch % 8 || a.v_row % 8 || a.v_head % 8 || a.v_batch % 8)
@@ -136,12 +138,15 @@ int fa_prepare(const p1x_attn_params* p, const float* q, const uint16_t* k, cons
         a.k_head = a.v_head = d * p->seq_kv;
         a.k_batch = a.v_batch = d * p->seq_kv * p->n_head_kv;
     }
-    // Bytes spanned by one head's seq_kv rows (the kernels' buffer range): 32-bit offsets.
-    const int64_t k_span = ((int64_t(p->seq_kv) - 1) * a.k_row + d) * 2, v_span = ((int64_t(p->seq_kv) - 1) * a.v_row + d) * 2;
-    if (k_span > 0x7ffffff0 || v_span > 0x7ffffff0)
-        return fail(P1X_EUNSUPPORTED, "one head's K or V rows must span less than 2 GiB");
-    a.k_bytes = uint32_t(k_span);
-    a.v_bytes = uint32_t(v_span);
+    if (kv_f16) {
+        // Bytes spanned by one head's seq_kv rows (the kernels' buffer range): 32-bit offsets.
+        const int64_t k_span = ((int64_t(p->seq_kv) - 1) * a.k_row + d) * 2;
+        const int64_t v_span = ((int64_t(p->seq_kv) - 1) * a.v_row + d) * 2;
+        if (k_span > 0x7ffffff0 || v_span > 0x7ffffff0)
+            return fail(P1X_EUNSUPPORTED, "one head's K or V rows must span less than 2 GiB");
+        a.k_bytes = uint32_t(k_span);
+        a.v_bytes = uint32_t(v_span);
+    }
     a.hq = p->n_head_q;
     a.hkv = p->n_head_kv;
     a.seq_q = p->seq_q;
@@ -285,7 +290,7 @@ int p1x_flash_attn_decode(const p1x_attn_params* p, const float* q, const uint16
                           size_t ws_bytes, void* stream) {
     if (int rc = ensure_init()) return rc;
     p1x::FaArgs a;
-    if (int rc = fa_prepare(p, q, k, v, strides, mask, nullptr, o, lse, ws, ws_bytes, a)) return rc;
+    if (int rc = fa_prepare(p, q, k, v, strides, mask, nullptr, o, lse, ws, ws_bytes, a, true)) return rc;
     hipError_t e = p1x::launch_fa_decode(a, p->batch, p->d_qk, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? P1X_OK : hip_fail(e, "flash_attn_decode");
 }
@@ -297,9 +302,54 @@ int p1x_flash_attn_decode_kvlen(const p1x_attn_params* p, const float* q, const 
     if (!kv_len) return fail(P1X_EINVAL, "null kv_len pointer");
     if (!aligned(kv_len, 4)) return fail(P1X_EINVAL, "kv_len must be 4-byte aligned");
     p1x::FaArgs a;
-    if (int rc = fa_prepare(p, q, k, v, strides, mask, kv_len, o, lse, ws, ws_bytes, a)) return rc;
+    if (int rc = fa_prepare(p, q, k, v, strides, mask, kv_len, o, lse, ws, ws_bytes, a, true)) return rc;
     hipError_t e = p1x::launch_fa_decode(a, p->batch, p->d_qk, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? P1X_OK : hip_fail(e, "flash_attn_decode_kvlen");
+}
+
+int p1x_flash_attn_decode_quant(const p1x_attn_params* p, int kv_type, const float* q, const void* k, const void* v,
+                                const p1x_kv_strides* byte_strides, const float* mask, const int32_t* kv_len, float* o,
+                                float* lse, void* ws, size_t ws_bytes, void* stream) {
+    if (int rc = ensure_init()) return rc;
+    if (kv_type != P1X_Q8_0 && kv_type != P1X_Q4_0)
+        return fail(P1X_EUNSUPPORTED, "quantized K/V must be q8_0 or q4_0");
+    if (int rc = p1x_attn_validate(p)) return rc;
+    if (!q || !k || !v || !o) return fail(P1X_EINVAL, "null q, k, v or o pointer");
+    if (p->d_qk != p->d_v || (p->d_qk != 64 && p->d_qk != 128 && p->d_qk != 256))
+        return fail(P1X_EUNSUPPORTED, "decode kernel supports d_qk == d_v in {64, 128, 256}");
+    if (kv_len && !aligned(kv_len, 4)) return fail(P1X_EINVAL, "kv_len must be 4-byte aligned");
+    const int64_t row_bytes = int64_t(p->d_qk) / 32 * (kv_type == P1X_Q8_0 ? 34 : 18);
+    p1x_kv_strides st;
+    if (byte_strides) {
+        st = *byte_strides;
+    } else {
+        st.k_row = st.v_row = row_bytes;
+        st.k_head = st.v_head = row_bytes * p->seq_kv;
+        st.k_batch = st.v_batch = row_bytes * p->seq_kv * p->n_head_kv;
+    }
+    if (st.k_row < row_bytes || st.v_row < row_bytes) return fail(P1X_EINVAL, "K/V row stride shorter than a row");
+    if (st.k_row % 4 || st.k_head % 4 || st.k_batch % 4 || st.v_row % 4 || st.v_head % 4 || st.v_batch % 4 ||
+        !aligned(k, 4) || !aligned(v, 4))
+        return fail(P1X_EINVAL, "quantized K/V rows, strides and base pointers must be 4-byte aligned");
+    p1x::FaArgs a;
+    if (int rc = fa_prepare(p, q, static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), nullptr, mask,
+                            kv_len, o, lse, ws, ws_bytes, a, false))
+        return rc;
+    const int64_t k_span = (int64_t(p->seq_kv) - 1) * st.k_row + row_bytes;
+    const int64_t v_span = (int64_t(p->seq_kv) - 1) * st.v_row + row_bytes;
+    if (k_span > 0x7ffffff0 || v_span > 0x7ffffff0)
+        return fail(P1X_EUNSUPPORTED, "one head's K or V rows must span less than 2 GiB");
+    a.kv_type = kv_type == P1X_Q8_0 ? 1 : 2;
+    a.kq = static_cast<const uint8_t*>(k);
+    a.vq = static_cast<const uint8_t*>(v);
+    a.k = nullptr;
+    a.v = nullptr;
+    a.k_row = st.k_row, a.k_head = st.k_head, a.k_batch = st.k_batch;
+    a.v_row = st.v_row, a.v_head = st.v_head, a.v_batch = st.v_batch;
+    a.k_bytes = uint32_t(k_span);
+    a.v_bytes = uint32_t(v_span);
+    hipError_t e = p1x::launch_fa_decode(a, p->batch, p->d_qk, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? P1X_OK : hip_fail(e, "flash_attn_decode_quant");
 }
 
 int p1x_round_to_fp16(const float* x, uint16_t* out, int64_t n, void* stream) {

@@ -29,6 +29,6 @@ int check_matvec(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K, i
 size_t fa_workspace(const p1x_attn_params* p);
 int fa_prepare(const p1x_attn_params* p, const float* q, const uint16_t* k, const uint16_t* v,
                const p1x_kv_strides* strides, const float* mask, const int32_t* kv_len, float* o, float* lse, void* ws,
-               size_t ws_bytes, FaArgs& a);
+               size_t ws_bytes, FaArgs& a, bool kv_f16 = true);
 
 }  // namespace p1x::capi

@@ -122,12 +122,61 @@ __device__ __forceinline__ void h8_to_f32(uint4 v, float* out) {
     }
 }
 
+// Quantized KV cache (llama.cpp -ctk/-ctv q8_0 / q4_0): each row of D values is D/32 GGUF blocks. A lane owns
+// 8 dimensions, a quarter (jq = lane % 4) of one block: its 16-byte load starts at the dword holding its
+// quants (q8_0: bytes 8 jq .. +7 of the block's 32; q4_0: bytes 8 (jq & 1) .. +7 of 16, low nibbles for
+// jq < 2, high for jq >= 2), and the block's first lane loads from the block start so it also holds the fp16
+// scale d, which the other three lanes of the quad take by DPP. Values are d * q (exact in FP32); the kernels
+// multiply the 8-term partial dot products by d (K) and fold d into p (V). Rows must be 4-byte aligned.
+enum { kKvF16 = 0, kKvQ8_0 = 1, kKvQ4_0 = 2 };
+template <int KT>
+struct KvQuant {
+    static constexpr int kBlockBytes = KT == kKvQ8_0 ? 34 : 18;
+    uint32_t load_off, qoff, doff, nib_shift;  // per-lane constants (rows are 4-byte aligned)
+    __device__ __forceinline__ explicit KvQuant(int l) {
+        const int blk = l >> 2, jq = l & 3;
+        const uint32_t boff = uint32_t(blk * kBlockBytes);
+        const uint32_t qstart = boff + 2 + 8 * uint32_t(KT == kKvQ8_0 ? jq : (jq & 1));
+        const uint32_t base = (jq == 0 ? boff : qstart) & ~3u;
+        load_off = base;
+        qoff = qstart - base;  // 0, 2 or 4
+        doff = boff - (boff & ~3u);
+        nib_shift = (KT == kKvQ4_0 && jq >= 2) ? 4u : 0u;
+    }
+    // The lane's 8 values (as exact small integers) and the block scale.
+    __device__ __forceinline__ void to_f32(uint4 w, float* out, float& d) const {
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+        const int i0 = int(qoff >> 2);
+        const uint32_t sel = (qoff & 2) ? 0x05040302u : 0x03020100u;
+        const uint32_t lo = __builtin_amdgcn_perm(i0 ? ww[2] : ww[1], i0 ? ww[1] : ww[0], sel);
+        const uint32_t hi = __builtin_amdgcn_perm(i0 ? ww[3] : ww[2], i0 ? ww[2] : ww[1], sel);
+        if constexpr (KT == kKvQ8_0) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                out[k] = float(int8_t((lo >> (8 * k)) & 0xffu));
+                out[4 + k] = float(int8_t((hi >> (8 * k)) & 0xffu));
+            }
+        } else {
+            const uint32_t l4 = (lo >> nib_shift) & 0x0F0F0F0Fu, h4 = (hi >> nib_shift) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                out[k] = float((l4 >> (8 * k)) & 0xffu) - 8.0f;
+                out[4 + k] = float((h4 >> (8 * k)) & 0xffu) - 8.0f;
+            }
+        }
+        const int d16 = int((w.x >> (8 * doff)) & 0xffffu);  // meaningful in the block's first lane
+        const int db = __builtin_amdgcn_update_dpp(0, d16, 0x00, 0xf, 0xf, true);  // quad_perm(0,0,0,0)
+        d = __half2float(__ushort_as_half(static_cast<unsigned short>(db)));
+    }
+};
+
 // Logits may exceed the wave's reference max by up to 2^kTau before the reference is raised (p <= 2^8).
 constexpr float kTau = 8.0f;
 
 // MODE bit 0: additive mask; bit 1: logit softcap. Compile-time, so the plain decode loop carries neither.
-template <int D, int NH, int MODE>
+template <int D, int NH, int MODE, int KT>
 __global__ __launch_bounds__(kSplitThreads) void k_fa_split(FaArgs a) {
+    static_assert(KT == kKvF16 || kDimsPerLane == 8, "quantized K/V need 8 dimensions per lane");
     constexpr bool kMask = (MODE & 1) != 0, kCap = (MODE & 2) != 0;
     constexpr int DPL = kDimsPerLane;   // dimensions per lane: DPL/8 chunks of 8 (one 16-byte load each)
     constexpr int CH = DPL / 8;
@@ -175,8 +224,16 @@ __global__ __launch_bounds__(kSplitThreads) void k_fa_split(FaArgs a) {
 #pragma unroll
         for (int d = 0; d < DPL; ++d) o[hh][d] = 0.0f;
     }
-    const auto krs = kv_rsrc(a.k + size_t(b) * a.k_batch + size_t(kvh) * a.k_head, a.k_bytes);
-    const auto vrs = kv_rsrc(a.v + size_t(b) * a.v_batch + size_t(kvh) * a.v_head, a.v_bytes);
+    // f16: element strides; quantized: byte strides from the byte pointers kq / vq.
+    const auto krs = KT == kKvF16 ? kv_rsrc(a.k + size_t(b) * a.k_batch + size_t(kvh) * a.k_head, a.k_bytes)
+                                  : kv_rsrc(reinterpret_cast<const __half*>(a.kq + size_t(b) * a.k_batch +
+                                                                            size_t(kvh) * a.k_head),
+                                            a.k_bytes);
+    const auto vrs = KT == kKvF16 ? kv_rsrc(a.v + size_t(b) * a.v_batch + size_t(kvh) * a.v_head, a.v_bytes)
+                                  : kv_rsrc(reinterpret_cast<const __half*>(a.vq + size_t(b) * a.v_batch +
+                                                                            size_t(kvh) * a.v_head),
+                                            a.v_bytes);
+    const KvQuant<KT == kKvF16 ? kKvQ8_0 : KT> kvq(l);
     const float* mrow = kMask ? a.mask + size_t(i) * a.seq_kv : nullptr;
 
     // Key of (batch t, slot u) for this lane's group: the GPW groups of a wave read GPW consecutive rows.
@@ -195,8 +252,13 @@ __global__ __launch_bounds__(kSplitThreads) void k_fa_split(FaArgs a) {
             const uint32_t j = uint32_t(key0 + t * KPB + u * GPW);
 #pragma unroll
             for (int c = 0; c < CH; ++c) {
-                bf.k[u][c] = ld_kv(krs, t < nb ? (j * uint32_t(a.k_row) + dim0(c)) * 2 : kOutOfRange);
-                bf.v[u][c] = ld_kv(vrs, t < nb ? (j * uint32_t(a.v_row) + dim0(c)) * 2 : kOutOfRange);
+                if constexpr (KT == kKvF16) {
+                    bf.k[u][c] = ld_kv(krs, t < nb ? (j * uint32_t(a.k_row) + dim0(c)) * 2 : kOutOfRange);
+                    bf.v[u][c] = ld_kv(vrs, t < nb ? (j * uint32_t(a.v_row) + dim0(c)) * 2 : kOutOfRange);
+                } else {
+                    bf.k[u][c] = ld_kv(krs, t < nb ? j * uint32_t(a.k_row) + kvq.load_off : kOutOfRange);
+                    bf.v[u][c] = ld_kv(vrs, t < nb ? j * uint32_t(a.v_row) + kvq.load_off : kOutOfRange);
+                }
             }
         }
     };
@@ -205,9 +267,13 @@ __global__ __launch_bounds__(kSplitThreads) void k_fa_split(FaArgs a) {
         float x[kKeys][NH];
 #pragma unroll
         for (int u = 0; u < kKeys; ++u) {
-            float kf[DPL];
+            float kf[DPL], dk = 1.0f;
+            if constexpr (KT == kKvF16) {
 #pragma unroll
-            for (int c = 0; c < CH; ++c) h8_to_f32(bf.k[u][c], kf + 8 * c);
+                for (int c = 0; c < CH; ++c) h8_to_f32(bf.k[u][c], kf + 8 * c);
+            } else {
+                kvq.to_f32(bf.k[u][0], kf, dk);
+            }
 #pragma unroll
             for (int hh = 0; hh < NH; ++hh) {
                 float d0 = 0.0f, d1 = 0.0f;
@@ -216,7 +282,7 @@ __global__ __launch_bounds__(kSplitThreads) void k_fa_split(FaArgs a) {
                     d0 = fmaf(qr[hh][d], kf[d], d0);
                     d1 = fmaf(qr[hh][DPL / 2 + d], kf[DPL / 2 + d], d1);
                 }
-                x[u][hh] = key_sum<LPK>(d0 + d1);
+                x[u][hh] = key_sum<LPK>(KT == kKvF16 ? d0 + d1 : (d0 + d1) * dk);
             }
             const int j = key0 + t * KPB + u * GPW;
             const bool ok = !kLast || j < j1;
@@ -252,11 +318,17 @@ __global__ __launch_bounds__(kSplitThreads) void k_fa_split(FaArgs a) {
                 mref[hh] = mn;
             }
         }
-        float vf[kKeys][DPL];
+        float vf[kKeys][DPL], dv[kKeys];
 #pragma unroll
-        for (int u = 0; u < kKeys; ++u)
+        for (int u = 0; u < kKeys; ++u) {
+            dv[u] = 1.0f;
+            if constexpr (KT == kKvF16) {
 #pragma unroll
-            for (int c = 0; c < CH; ++c) h8_to_f32(bf.v[u][c], vf[u] + 8 * c);
+                for (int c = 0; c < CH; ++c) h8_to_f32(bf.v[u][c], vf[u] + 8 * c);
+            } else {
+                kvq.to_f32(bf.v[u][0], vf[u], dv[u]);
+            }
+        }
 #pragma unroll
         for (int hh = 0; hh < NH; ++hh) {
             // Masks can leave every key so far at -inf: then the reference is -inf and p must be 0.
@@ -266,6 +338,7 @@ __global__ __launch_bounds__(kSplitThreads) void k_fa_split(FaArgs a) {
             for (int u = 0; u < kKeys; ++u) {
                 p[u] = __builtin_amdgcn_exp2f(x[u][hh] - base);
                 s[hh] += p[u];
+                if constexpr (KT != kKvF16) p[u] *= dv[u];  // d of the lane's V block folded into p
             }
 #pragma unroll
             for (int d = 0; d < DPL; ++d) {
@@ -502,14 +575,14 @@ __global__ __launch_bounds__(256) void k_fa_combine(FaArgs a, int rows) {
     if (a.oq) q8_1_row<CPL>(ov, size_t(row) * D + CPL * lane, a.oq, a.ods);
 }
 
-template <int D, int NH>
+template <int D, int NH, int KT>
 hipError_t launch_split(const FaArgs& a, int batch, hipStream_t stream) {
     const dim3 grid(a.splits, batch * a.hkv * a.head_chunks, a.seq_q);
     switch ((a.mask ? 1 : 0) | (a.softcap > 0.0f ? 2 : 0)) {
-        case 0: hipLaunchKernelGGL((k_fa_split<D, NH, 0>), grid, dim3(kSplitThreads), 0, stream, a); break;
-        case 1: hipLaunchKernelGGL((k_fa_split<D, NH, 1>), grid, dim3(kSplitThreads), 0, stream, a); break;
-        case 2: hipLaunchKernelGGL((k_fa_split<D, NH, 2>), grid, dim3(kSplitThreads), 0, stream, a); break;
-        default: hipLaunchKernelGGL((k_fa_split<D, NH, 3>), grid, dim3(kSplitThreads), 0, stream, a); break;
+        case 0: hipLaunchKernelGGL((k_fa_split<D, NH, 0, KT>), grid, dim3(kSplitThreads), 0, stream, a); break;
+        case 1: hipLaunchKernelGGL((k_fa_split<D, NH, 1, KT>), grid, dim3(kSplitThreads), 0, stream, a); break;
+        case 2: hipLaunchKernelGGL((k_fa_split<D, NH, 2, KT>), grid, dim3(kSplitThreads), 0, stream, a); break;
+        default: hipLaunchKernelGGL((k_fa_split<D, NH, 3, KT>), grid, dim3(kSplitThreads), 0, stream, a); break;
     }
     if (a.splits == 1) return hipGetLastError();  // the split pass wrote O and LSE
     const int rows = batch * a.hq * a.seq_q;
@@ -518,12 +591,21 @@ hipError_t launch_split(const FaArgs& a, int batch, hipStream_t stream) {
     return hipGetLastError();
 }
 
-template <int D>
+template <int D, int KT>
 hipError_t launch_d(const FaArgs& a, int batch, int nh, hipStream_t stream) {
     switch (nh) {
-        case 1: return launch_split<D, 1>(a, batch, stream);
-        case 2: return launch_split<D, 2>(a, batch, stream);
-        case 4: return launch_split<D, 4>(a, batch, stream);
+        case 1: return launch_split<D, 1, KT>(a, batch, stream);
+        case 2: if constexpr (P1X_FA_MAX_NH >= 2) return launch_split<D, 2, KT>(a, batch, stream); break;
+        case 4: if constexpr (P1X_FA_MAX_NH >= 4) return launch_split<D, 4, KT>(a, batch, stream); break;
+    }
+    return hipErrorInvalidValue;
+}
+template <int KT>
+hipError_t launch_kt(const FaArgs& a, int batch, int d, int nh, hipStream_t stream) {
+    switch (d) {
+        case 64: return launch_d<64, KT>(a, batch, nh, stream);
+        case 128: return launch_d<128, KT>(a, batch, nh, stream);
+        case 256: return launch_d<256, KT>(a, batch, nh, stream);
     }
     return hipErrorInvalidValue;
 }
@@ -557,10 +639,10 @@ void fa_split_plan(int batch, int hq, int hkv, int seq_q, int seq_kv, int d, int
 hipError_t launch_fa_decode(FaArgs a, int batch, int d, hipStream_t stream) {
     const int nh = fa_heads_per_wg(a.hq, a.hkv);
     a.head_chunks = (a.hq / a.hkv) / nh;
-    switch (d) {
-        case 64: return launch_d<64>(a, batch, nh, stream);
-        case 128: return launch_d<128>(a, batch, nh, stream);
-        case 256: return launch_d<256>(a, batch, nh, stream);
+    switch (a.kv_type) {
+        case kKvF16: return launch_kt<kKvF16>(a, batch, d, nh, stream);
+        case kKvQ8_0: return launch_kt<kKvQ8_0>(a, batch, d, nh, stream);
+        case kKvQ4_0: return launch_kt<kKvQ4_0>(a, batch, d, nh, stream);
     }
     return hipErrorInvalidValue;
 }

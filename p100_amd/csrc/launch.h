@@ -38,6 +38,8 @@ struct FaArgs {
     const int* kv_len;  // optional device int: valid KV rows at execution time (<= seq_kv); null = seq_kv
     int8_t* oq;         // optional: Q8_1 of o (qs [rows * D], ds float4 [rows * D / 32]) written by the combine
     float4* ods;
+    int kv_type;              // 0 fp16 (k, v, element strides); 1 q8_0, 2 q4_0 (kq, vq, byte strides)
+    const uint8_t *kq, *vq;
     int64_t k_row, k_head, k_batch, v_row, v_head, v_batch;  // element strides
     uint32_t k_bytes, v_bytes;  // bytes spanned by one head's seq_kv rows of K and of V
     int hq, hkv, seq_q, seq_kv, causal, splits, chunk, head_chunks;
