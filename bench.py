@@ -229,10 +229,11 @@ def measure_roofline(torch, P, lib, timer, layers, x):
     rec = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
     if os.path.exists(rec):
         with open(rec) as f:
-            t = json.load(f).get("k_mmvq q4_0 4096x14336 ne11=1")
+            t = json.load(f).get("k_mmvr q4_0 4096x14336 ne11=1")
         if t:
             traffic, src = t["traffic_bytes"], t["source"]
-    return {"kernel": "k_mmvq<q4_0> 4096x14336 (prepared Q8_1 activation)", "bound": "hbm",
+    return {"kernel": "k_mmvr<q4_0> 4096x14336 (prepared Q8_1 activation held in registers; row-groups of 4 waves "
+                      "x 4 rows, 2 units per lane)", "bound": "hbm",
             "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4),
             "traffic": traffic, "traffic_unit": "bytes per launch", "traffic_source": src,
             "algorithmic_bytes": b, "avg_us": round(med, 3), "min_us": round(mn, 3)}

@@ -13,6 +13,9 @@
 // RW rows and B columns reuse each decoded weight. Units past the row end are clamped to a valid unit and their
 // result dropped by a select, so the bodies stay branch-free. Lane partials are reduced with DPP and two
 // cross-row swizzles; four independent waves form a 256-thread work-group.
+//
+// One column of q4_0 / q8_0 on a prepared activation takes k_mmvr instead: the activation is held in registers by
+// row-groups of 1-4 waves that split K, so there is no LDS copy and no barrier ahead of the weight stream.
 #include "common.h"
 #include "launch.h"
 
@@ -36,6 +39,9 @@
 #endif
 #ifndef P1X_MMVQ_MAX_RW
 #define P1X_MMVQ_MAX_RW 4
+#endif
+#ifndef P1X_MMVR_ENABLE
+#define P1X_MMVR_ENABLE 1  // one prepared q4_0 / q8_0 column: register-resident activation kernel (k_mmvr)
 #endif
 
 namespace p1x {
@@ -439,6 +445,125 @@ __global__ __launch_bounds__(256) void k_mmvq_fx(const uint8_t* __restrict__ w, 
         w, nb01, M, K, y, gs);
 }
 
+// One activation column on a prepared Q8_1 activation (q4_0 / q8_0): the activation stays in registers. A row-group
+// of NWK waves owns R consecutive rows; its thread t owns units t + 64*NWK*j (j < UPT) of every one of them, loads
+// those units' Q8_1 blocks once, then requests all R x UPT weight units together and computes them. Row sums are
+// reduced by DPP inside each wave and, for NWK > 1, through LDS across the row-group's waves. Nothing is staged in
+// LDS and no barrier precedes the compute: a work-group reads the activation (48 bytes per 32-block) once, straight
+// from L2 into registers, and the weight stream starts in the same round trip. Units past the row end are clamped
+// to unit 0 and dropped by a select; rows past M are clamped for the loads and never stored.
+template <int TYPE, int NWK, int UPT, int R, bool SUMS>
+__global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int64_t nb01, int M, int K,
+                                              const int8_t* __restrict__ xq, const float4* __restrict__ xds,
+                                              float* __restrict__ y, int32_t* __restrict__ gs) {
+    using U = typename UnitOf<TYPE>::T;
+    static_assert(U::kActBlocks == 1 && U::kGroups == 1, "one Q8_1 block and one int32 sum per unit");
+    constexpr int T = 64 * NWK, G = 4 / NWK;
+    __shared__ float red[4][R];
+    const int tid = threadIdx.x, g = tid / T, t = tid - g * T;
+    const int units = K / U::kElems;
+    const int row0 = (blockIdx.x * G + g) * R;
+    const ActGlobal act{xq, xds, K};
+    ActBlock x[UPT];
+    int uc[UPT];
+    bool uok[UPT];
+#pragma unroll
+    for (int j = 0; j < UPT; ++j) {
+        const int u = t + T * j;
+        uok[j] = u < units;
+        uc[j] = uok[j] ? u : 0;
+        x[j] = act.get(0, uc[j]);
+    }
+    U wv[R][UPT];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint8_t* wr = w + size_t(min(row0 + r, M - 1)) * nb01;
+#pragma unroll
+        for (int j = 0; j < UPT; ++j) wv[r][j].load(wr, uc[j]);
+    }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float a = 0.0f;
+#pragma unroll
+        for (int j = 0; j < UPT; ++j) {
+            int32_t gg[1];
+            const float v = wv[r][j].acc(&x[j], a, gg);
+            a = uok[j] ? v : a;
+            if (SUMS && uok[j] && row0 + r < M) gs[size_t(row0 + r) * units + t + T * j] = gg[0];
+        }
+        acc[r] = wave_total(a);
+    }
+    const int lane = tid & 63;
+    if constexpr (NWK == 1) {
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (row0 + r < M) y[row0 + r] = acc[r];
+        }
+    } else {
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) red[tid >> 6][r] = acc[r];
+        }
+        __syncthreads();
+        if (t < R && row0 + t < M) {
+            float sum = red[g * NWK][t];
+#pragma unroll
+            for (int k = 1; k < NWK; ++k) sum += red[g * NWK + k][t];
+            y[row0 + t] = sum;
+        }
+    }
+}
+
+// Row-group shape of k_mmvr (measured on the Llama-3-8B matrices, graph launches): waves per row-group and units
+// per thread cover the row (at most 512 units), rows per row-group keep the weight loads in flight per thread at
+// 2-8 units. Returns false when the row is too long for the register form.
+struct MmvrPlan {
+    int nwk, upt, r;
+};
+bool mmvr_plan(int type, int M, int K, MmvrPlan& p) {
+    const int units = K / 32;
+    if (units <= 64) {
+        p = {1, 1, 2};
+    } else if (units <= 128) {
+        const bool split = type == Q4_0 ? M >= 20000 : (M >= 8192 || M <= 1024);
+        p = split ? MmvrPlan{2, 1, type == Q4_0 ? 4 : 2} : MmvrPlan{1, 2, M <= 1024 ? 1 : 2};
+    } else if (units <= 256) {
+        p = {2, 2, 2};
+    } else if (units <= 512) {
+        p = {4, 2, 4};
+    } else {
+        return false;
+    }
+    return true;
+}
+
+template <int TYPE>
+hipError_t launch_mmvr(const MmvrPlan& p, const uint8_t* w, int64_t nb01, int M, int K, const int8_t* xq,
+                       const float4* xds, float* y, int32_t* gs, hipStream_t stream) {
+#define P1X_MMVR(NW, UP, RR)                                                                                        \
+    if (p.nwk == NW && p.upt == UP && p.r == RR) {                                                                 \
+        const dim3 grid((M + (4 / NW) * RR - 1) / ((4 / NW) * RR));                                                \
+        if (gs)                                                                                                    \
+            hipLaunchKernelGGL((k_mmvr<TYPE, NW, UP, RR, true>), grid, dim3(256), 0, stream, w, nb01, M, K, xq, xds, y, \
+                               gs);                                                                                \
+        else                                                                                                       \
+            hipLaunchKernelGGL((k_mmvr<TYPE, NW, UP, RR, false>), grid, dim3(256), 0, stream, w, nb01, M, K, xq, xds, y, \
+                               gs);                                                                                \
+        return hipGetLastError();                                                                                  \
+    }
+    P1X_MMVR(1, 1, 2)
+    P1X_MMVR(1, 2, 1)
+    P1X_MMVR(1, 2, 2)
+    P1X_MMVR(2, 1, 2)
+    P1X_MMVR(2, 1, 4)
+    P1X_MMVR(2, 2, 2)
+    P1X_MMVR(4, 2, 4)
+#undef P1X_MMVR
+    return hipErrorInvalidValue;
+}
+
 template <int TYPE, int B>
 hipError_t launch_b(const uint8_t* w, int64_t nb01, int M, int K, int rw, const int8_t* xq, const float4* xds,
                     const float* x, float* y, int32_t* gs, hipStream_t stream) {
@@ -514,6 +639,10 @@ hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int 
     const int rw = mmvq_rows_per_wave(M, B, x != nullptr);
     const auto* wb = static_cast<const uint8_t*>(w);
     const auto* d4 = reinterpret_cast<const float4*>(xds);
+    MmvrPlan plan;
+    if (B == 1 && !x && P1X_MMVR_ENABLE && (type == Q4_0 || type == Q8_0) && mmvr_plan(type, M, K, plan))
+        return type == Q4_0 ? launch_mmvr<Q4_0>(plan, wb, nb01, M, K, xq, d4, y, gs, stream)
+                            : launch_mmvr<Q8_0>(plan, wb, nb01, M, K, xq, d4, y, gs, stream);
     switch (type) {
         case Q4_0: return launch_type<Q4_0>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
         case Q8_0: return launch_type<Q8_0>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);

@@ -151,7 +151,9 @@ def test_mmvq_parity(orc, gpu, tname):
             y2 = P.mul_mat_vec(t, to_dev(w), 17, k, to_dev(x), act="q8_1").cpu().numpy()
             y3 = P.mul_mat_vec(t, to_dev(w), 17, k, P.quantize_q8_1(to_dev(x))).cpu().numpy()
             assert (y2.view(np.uint32) == y.cpu().numpy().view(np.uint32)).all()
-            assert (y3.view(np.uint32) == y2.view(np.uint32)).all()
+            # One q4_0 / q8_0 column on a prepared activation runs the register-resident kernel, whose FP32 partial
+            # sums are grouped differently from the single-launch kernel's: the same bars, not the same bits.
+            check_matvec(orc, t, w, x, y3, None, "q81")
     print(f"{tname} q81 worst |y-exact|/(|w||x|) = {worst:.3e}")
 
 
@@ -213,6 +215,35 @@ def test_h16_single_block_is_bit_exact(orc, gpu):
         ref = orc.mul_mat_vec(t, w, 33, nb, x, mode="h16")
         if nb == 32:
             assert (y.view(np.uint32) == ref.view(np.uint32)).all(), tname
+
+
+# (rows, K) chosen so that every row-group shape of the one-column register kernel runs (K of 1 / 2 / 4 / 8 / 16
+# blocks of 64 units per wave row, rows below and above the plan thresholds, ragged last work-groups), plus K past
+# its 512-unit limit (the LDS kernel).
+REGISTER_CASES = [(5, 32), (17, 2048), (1023, 4096), (1029, 4096), (8195, 4096), (20003, 4096), (37, 6144),
+                  (41, 8192), (45, 14336), (43, 16384), (19, 16416)]
+
+
+@pytest.mark.parametrize("tname", ["q4_0", "q8_0"])
+def test_one_column_register_kernel(orc, gpu, tname):
+    """One column on a prepared Q8_1 activation: int32 group sums bit-exact, FP32 within the bars, the group-sum
+    export leaving the FP32 result unchanged, and a padded row stride."""
+    import p100_amd as P
+
+    t = orc.TYPES[tname]
+    for rows, k in REGISTER_CASES:
+        w, x = make_case(orc, t, k, rows, 1, seed=31000 + rows + k)
+        q = P.quantize_q8_1(to_dev(x))
+        y, sums = P.mul_mat_vec(t, to_dev(w), rows, k, q, group_sums=True)
+        check_matvec(orc, t, w, x, y.cpu().numpy(), sums.cpu().numpy(), "q81")
+        y2 = P.mul_mat_vec(t, to_dev(w), rows, k, q).cpu().numpy()
+        assert (y2.view(np.uint32) == y.cpu().numpy().view(np.uint32)).all(), (rows, k)
+        if rows in (1029, 45):
+            rb = w.shape[1]
+            pad = np.zeros((rows, rb + 6), np.uint8)
+            pad[:, :rb] = w
+            y3 = P.mul_mat_vec(t, to_dev(pad), rows, k, q, nb01=rb + 6).cpu().numpy()
+            assert (y3.view(np.uint32) == y2.view(np.uint32)).all(), (rows, k)
 
 
 @pytest.mark.parametrize("tname", TYPES)
