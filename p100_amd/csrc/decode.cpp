@@ -208,6 +208,11 @@ int p1x_llama_decode_step(const p1x_llama_model* m, p1x_decode_state* state, con
         fa.ods = reinterpret_cast<float4*>(ds);
     }
     const bool wo_fused = !wo_prepared && p1x::mmvq_fused_fits(1, E, E);
+    // RoPE and the KV append ride on the q/k/v projection when its register-resident kernel applies to every
+    // part of the stack (q rows and k / v rows), else they take their own launch.
+    const bool rope_fused = p1x::mmvq_rope_kv_supported(hp.wtype, E + 2 * kv, E, d) &&
+                            p1x::mmvq_rope_kv_supported(hp.wtype, E, E, d) &&
+                            p1x::mmvq_rope_kv_supported(hp.wtype, kv, E, d);
 
     hipError_t e = hipSuccess;
 #define P1X_TRY(call, what)                         \
@@ -221,16 +226,31 @@ int p1x_llama_decode_step(const p1x_llama_model* m, p1x_decode_state* state, con
         P1X_TRY(p1x::launch_rms_norm_q8_1(x, l ? y : nullptr, L.attn_norm, E, hp.rms_eps, qs, ds, nullptr, s),
                 "attention norm");
         const auto* wq = static_cast<const uint8_t*>(L.wq);
-        if (L.wk == wq + E * nb_w && L.wv == wq + (E + kv) * nb_w) {
-            P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, wq, nb_w, E + 2 * kv, E, qs, ds, nullptr, qkv, nullptr, s), "qkv");
+        const bool stacked = L.wk == wq + E * nb_w && L.wv == wq + (E + kv) * nb_w;
+        if (rope_fused) {  // the projection rotates q / k and appends k / v itself
+            p1x::RopeKv rk{qr, L.k_cache, L.v_cache, int(E), int(kv), d, hp.n_ctx, 0, &state->pos, theta_scale};
+            if (stacked) {
+                P1X_TRY(p1x::launch_mmvq_rope_kv(hp.wtype, wq, nb_w, E + 2 * kv, E, qs, ds, rk, s), "qkv + rope");
+            } else {
+                P1X_TRY(p1x::launch_mmvq_rope_kv(hp.wtype, L.wq, nb_w, E, E, qs, ds, rk, s), "q + rope");
+                rk.row_base = int(E);
+                P1X_TRY(p1x::launch_mmvq_rope_kv(hp.wtype, L.wk, nb_w, kv, E, qs, ds, rk, s), "k + rope");
+                rk.row_base = int(E + kv);
+                P1X_TRY(p1x::launch_mmvq_rope_kv(hp.wtype, L.wv, nb_w, kv, E, qs, ds, rk, s), "v");
+            }
         } else {
-            P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, L.wq, nb_w, E, E, qs, ds, nullptr, qkv, nullptr, s), "q");
-            P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, L.wk, nb_w, kv, E, qs, ds, nullptr, qkv + E, nullptr, s), "k");
-            P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, L.wv, nb_w, kv, E, qs, ds, nullptr, qkv + E + kv, nullptr, s), "v");
+            if (stacked) {
+                P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, wq, nb_w, E + 2 * kv, E, qs, ds, nullptr, qkv, nullptr, s), "qkv");
+            } else {
+                P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, L.wq, nb_w, E, E, qs, ds, nullptr, qkv, nullptr, s), "q");
+                P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, L.wk, nb_w, kv, E, qs, ds, nullptr, qkv + E, nullptr, s), "k");
+                P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, L.wv, nb_w, kv, E, qs, ds, nullptr, qkv + E + kv, nullptr, s),
+                        "v");
+            }
+            P1X_TRY(p1x::launch_rope_kv_append(qkv, qkv + E, qkv + E + kv, qr, L.k_cache, L.v_cache, hp.n_head,
+                                               hp.n_head_kv, d, hp.n_ctx, &state->pos, theta_scale, s),
+                    "rope + kv append");
         }
-        P1X_TRY(p1x::launch_rope_kv_append(qkv, qkv + E, qkv + E + kv, qr, L.k_cache, L.v_cache, hp.n_head, hp.n_head_kv,
-                                           d, hp.n_ctx, &state->pos, theta_scale, s),
-                "rope + kv append");
         fa.k = reinterpret_cast<const __half*>(L.k_cache);
         fa.v = reinterpret_cast<const __half*>(L.v_cache);
         P1X_TRY(p1x::launch_fa_decode(fa, 1, d, s), "attention");

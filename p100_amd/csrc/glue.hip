@@ -173,13 +173,11 @@ __global__ __launch_bounds__(256) void k_rope_kv_append(const float* __restrict_
     const bool is_q = t < nq;
     const int u = is_q ? t : t - nq, h = u / half, p = u % half;
     const float2 x = *reinterpret_cast<const float2*>((is_q ? q : k) + size_t(h) * d + 2 * p);
-    const float theta = float(pos) * powf(theta_scale, float(p));
-    const float c = cosf(theta), s = sinf(theta);
-    const float y0 = x.x * c - x.y * s, y1 = x.x * s + x.y * c;
+    const float2 r = rope_pair(x.x, x.y, pos, p, theta_scale);
     if (is_q) {
-        *reinterpret_cast<float2*>(q_out + size_t(h) * d + 2 * p) = make_float2(y0, y1);
+        *reinterpret_cast<float2*>(q_out + size_t(h) * d + 2 * p) = r;
     } else if (row_ok) {
-        *reinterpret_cast<__half2*>(k_cache + (size_t(h) * n_ctx + pos) * d + 2 * p) = __floats2half2_rn(y0, y1);
+        *reinterpret_cast<__half2*>(k_cache + (size_t(h) * n_ctx + pos) * d + 2 * p) = __floats2half2_rn(r.x, r.y);
     }
 }
 

@@ -14,6 +14,21 @@ hipError_t launch_round_fp16(const float* x, uint16_t* out, int64_t n, hipStream
 hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
                        const float* x, float* y, int32_t* gs, hipStream_t stream);
 bool mmvq_fused_fits(int B, int M, int K);
+// One token's q/k/v projection (one column, prepared Q8_1) with llama.cpp normal-mode RoPE and the KV-cache append
+// done by the mat-vec itself: rows [0, E) of the stacked q/k/v weights are q (rotated into q_out), [E, E+kv) k
+// (rotated, fp16 into k_cache [n_head_kv][n_ctx][d] at *pos), [E+kv, E+2kv) v (fp16 into v_cache); a launch covers
+// rows row_base .. row_base+M-1 of that stack. Cache rows are written only for 0 <= *pos < n_ctx, as
+// launch_rope_kv_append does.
+struct RopeKv {
+    float* q_out;
+    uint16_t *k_cache, *v_cache;
+    int E, kv, d, n_ctx, row_base;
+    const int* pos;
+    float theta_scale;
+};
+bool mmvq_rope_kv_supported(int type, int M, int K, int d);
+hipError_t launch_mmvq_rope_kv(int type, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
+                               const RopeKv& rk, hipStream_t stream);
 // Several activation columns on int8 matrix cores (mmq.hip): q4_0 / q8_0 weights, 1..kMmqMaxCols columns of a
 // prepared Q8_1 activation.
 constexpr int kMmqMaxCols = 16;

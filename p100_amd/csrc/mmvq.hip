@@ -452,10 +452,40 @@ __global__ __launch_bounds__(256) void k_mmvq_fx(const uint8_t* __restrict__ w, 
 // LDS and no barrier precedes the compute: a work-group reads the activation (48 bytes per 32-block) once, straight
 // from L2 into registers, and the weight stream starts in the same round trip. Units past the row end are clamped
 // to unit 0 and dropped by a select; rows past M are clamped for the loads and never stored.
-template <int TYPE, int NWK, int UPT, int R, bool SUMS>
+// Epilogues of k_mmvr: the row sums stored as they are, or one token's q/k/v rows rotated in adjacent pairs and
+// appended to the KV cache (RopeKv; R is even there, so a row-group holds whole pairs).
+struct EpiRows {
+    static constexpr bool kPairs = false;
+    float* y;
+    __device__ __forceinline__ void row(int r, float v, int M) const {
+        if (r < M) y[r] = v;
+    }
+};
+struct EpiRopeKv {
+    static constexpr bool kPairs = true;
+    RopeKv a;
+    __device__ __forceinline__ void pair(int r, float v0, float v1, int M) const {
+        if (r >= M) return;
+        const int g = a.row_base + r, pos = *a.pos;
+        const bool row_ok = pos >= 0 && pos < a.n_ctx;
+        if (g < a.E) {
+            const int i = g % a.d;
+            *reinterpret_cast<float2*>(a.q_out + g) = rope_pair(v0, v1, pos, i >> 1, a.theta_scale);
+        } else if (row_ok) {
+            const bool is_k = g < a.E + a.kv;
+            const int u = g - a.E - (is_k ? 0 : a.kv), h = u / a.d, i = u - h * a.d;
+            const float2 o = is_k ? rope_pair(v0, v1, pos, i >> 1, a.theta_scale) : make_float2(v0, v1);
+            __half* cache = reinterpret_cast<__half*>(is_k ? a.k_cache : a.v_cache);
+            *reinterpret_cast<__half2*>(cache + (size_t(h) * a.n_ctx + pos) * a.d + i) = __floats2half2_rn(o.x, o.y);
+        }
+    }
+};
+
+template <int TYPE, int NWK, int UPT, int R, bool SUMS, class EPI>
 __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int64_t nb01, int M, int K,
                                               const int8_t* __restrict__ xq, const float4* __restrict__ xds,
-                                              float* __restrict__ y, int32_t* __restrict__ gs) {
+                                              const EPI epi, int32_t* __restrict__ gs) {
+    static_assert(!EPI::kPairs || R % 2 == 0, "row pairs stay inside one row-group");
     using U = typename UnitOf<TYPE>::T;
     static_assert(U::kActBlocks == 1 && U::kGroups == 1, "one Q8_1 block and one int32 sum per unit");
     constexpr int T = 64 * NWK, G = 4 / NWK;
@@ -498,8 +528,12 @@ __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int
     if constexpr (NWK == 1) {
         if (lane == 0) {
 #pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (row0 + r < M) y[row0 + r] = acc[r];
+            for (int r = 0; r < R; r += EPI::kPairs ? 2 : 1) {
+                if constexpr (EPI::kPairs)
+                    epi.pair(row0 + r, acc[r], acc[r + 1], M);
+                else
+                    epi.row(row0 + r, acc[r], M);
+            }
         }
     } else {
         if (lane == 0) {
@@ -507,11 +541,17 @@ __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int
             for (int r = 0; r < R; ++r) red[tid >> 6][r] = acc[r];
         }
         __syncthreads();
-        if (t < R && row0 + t < M) {
-            float sum = red[g * NWK][t];
+        float sum = 0.0f;  // row t of the row-group, summed by lane t < R of its first wave
+        if (t < R) {
+            sum = red[g * NWK][t];
 #pragma unroll
             for (int k = 1; k < NWK; ++k) sum += red[g * NWK + k][t];
-            y[row0 + t] = sum;
+        }
+        if constexpr (EPI::kPairs) {
+            const float next = __shfl_down(sum, 1);  // every lane of the wave takes part
+            if (t < R && !(t & 1)) epi.pair(row0 + t, sum, next, M);
+        } else if (t < R) {
+            epi.row(row0 + t, sum, M);
         }
     }
 }
@@ -539,22 +579,24 @@ bool mmvr_plan(int type, int M, int K, MmvrPlan& p) {
     return true;
 }
 
-template <int TYPE>
+template <int TYPE, class EPI>
 hipError_t launch_mmvr(const MmvrPlan& p, const uint8_t* w, int64_t nb01, int M, int K, const int8_t* xq,
-                       const float4* xds, float* y, int32_t* gs, hipStream_t stream) {
+                       const float4* xds, const EPI& epi, int32_t* gs, hipStream_t stream) {
 #define P1X_MMVR(NW, UP, RR)                                                                                        \
     if (p.nwk == NW && p.upt == UP && p.r == RR) {                                                                 \
         const dim3 grid((M + (4 / NW) * RR - 1) / ((4 / NW) * RR));                                                \
         if (gs)                                                                                                    \
-            hipLaunchKernelGGL((k_mmvr<TYPE, NW, UP, RR, true>), grid, dim3(256), 0, stream, w, nb01, M, K, xq, xds, y, \
-                               gs);                                                                                \
+            hipLaunchKernelGGL((k_mmvr<TYPE, NW, UP, RR, true, EPI>), grid, dim3(256), 0, stream, w, nb01, M, K, xq, xds, \
+                               epi, gs);                                                                           \
         else                                                                                                       \
-            hipLaunchKernelGGL((k_mmvr<TYPE, NW, UP, RR, false>), grid, dim3(256), 0, stream, w, nb01, M, K, xq, xds, y, \
-                               gs);                                                                                \
+            hipLaunchKernelGGL((k_mmvr<TYPE, NW, UP, RR, false, EPI>), grid, dim3(256), 0, stream, w, nb01, M, K, xq,   \
+                               xds, epi, gs);                                                                      \
         return hipGetLastError();                                                                                  \
     }
     P1X_MMVR(1, 1, 2)
-    P1X_MMVR(1, 2, 1)
+    if constexpr (!EPI::kPairs) {
+        P1X_MMVR(1, 2, 1)
+    }
     P1X_MMVR(1, 2, 2)
     P1X_MMVR(2, 1, 2)
     P1X_MMVR(2, 1, 4)
@@ -641,8 +683,8 @@ hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int 
     const auto* d4 = reinterpret_cast<const float4*>(xds);
     MmvrPlan plan;
     if (B == 1 && !x && P1X_MMVR_ENABLE && (type == Q4_0 || type == Q8_0) && mmvr_plan(type, M, K, plan))
-        return type == Q4_0 ? launch_mmvr<Q4_0>(plan, wb, nb01, M, K, xq, d4, y, gs, stream)
-                            : launch_mmvr<Q8_0>(plan, wb, nb01, M, K, xq, d4, y, gs, stream);
+        return type == Q4_0 ? launch_mmvr<Q4_0>(plan, wb, nb01, M, K, xq, d4, EpiRows{y}, gs, stream)
+                            : launch_mmvr<Q8_0>(plan, wb, nb01, M, K, xq, d4, EpiRows{y}, gs, stream);
     switch (type) {
         case Q4_0: return launch_type<Q4_0>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
         case Q8_0: return launch_type<Q8_0>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
@@ -650,6 +692,22 @@ hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int 
         case Q6_K: return launch_type<Q6_K>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
     }
     return hipErrorInvalidValue;
+}
+
+bool mmvq_rope_kv_supported(int type, int M, int K, int d) {
+    MmvrPlan plan;
+    return P1X_MMVR_ENABLE && (type == Q4_0 || type == Q8_0) && M % 2 == 0 && d % 2 == 0 && mmvr_plan(type, M, K, plan);
+}
+
+hipError_t launch_mmvq_rope_kv(int type, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
+                               const RopeKv& rk, hipStream_t stream) {
+    MmvrPlan plan;
+    if (!mmvq_rope_kv_supported(type, M, K, rk.d) || !mmvr_plan(type, M, K, plan)) return hipErrorInvalidValue;
+    if (plan.r == 1) plan.r = 2;  // the same per-row arithmetic (rows never share sums), whole pairs per row-group
+    const auto* wb = static_cast<const uint8_t*>(w);
+    const auto* d4 = reinterpret_cast<const float4*>(xds);
+    return type == Q4_0 ? launch_mmvr<Q4_0>(plan, wb, nb01, M, K, xq, d4, EpiRopeKv{rk}, nullptr, stream)
+                        : launch_mmvr<Q8_0>(plan, wb, nb01, M, K, xq, d4, EpiRopeKv{rk}, nullptr, stream);
 }
 
 }  // namespace p1x
