@@ -198,8 +198,11 @@ __global__ __launch_bounds__(kSplitThreads) void k_fa_split(FaArgs a) {
     // n_kv <= seq_kv valid rows at execution time (the split plan covers all seq_kv).
     const int n_kv = a.kv_len ? min(max(*a.kv_len, 0), a.seq_kv) : a.seq_kv;
     const int j_end = a.causal ? min(n_kv, i + (n_kv - a.seq_q) + 1) : n_kv;
-    const int j0 = split * a.chunk;
-    const int j1 = min(j0 + a.chunk, j_end);
+    // With a device-side length the plan was made for the capacity: the chunk is re-derived from the length
+    // actually visible (whole batches, spread over all the planned splits; splits past it get no keys).
+    const int chunk = a.kv_len ? (n_kv + a.splits * KPB - 1) / (a.splits * KPB) * KPB : a.chunk;
+    const int j0 = split * chunk;
+    const int j1 = min(j0 + chunk, j_end);
 
     const float qmul = kCap ? a.scale : a.scale * kLog2e;
     float qr[NH][DPL];

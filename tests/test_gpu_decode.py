@@ -228,11 +228,14 @@ def test_flash_attn_kvlen_matches_reference(orc, gpu, seq_q, causal):
     assert not o.any() and bool(torch.isneginf(lse).all())
 
 
-def test_flash_attn_kvlen_graph_replay(orc, gpu):
-    """One captured launch serves every length: the length tensor changes between replays."""
+@pytest.mark.parametrize("cap,lengths", [(768, [513, 600, 767, 768, 1]), (8192, [600, 8192, 4097, 65, 1])])
+def test_flash_attn_kvlen_graph_replay(orc, gpu, cap, lengths):
+    """One captured launch serves every length: the length tensor changes between replays. The plan is made
+    for the capacity; the kernels spread the visible length over all its splits (a short length in a large
+    cache still uses every split)."""
     import torch
 
-    cap, hq, hkv, d = 768, 32, 8, 128
+    hq, hkv, d = 32, 8, 128
     rng = np.random.default_rng(3)
     q = rng.standard_normal(hq * d).astype(np.float32)
     k16 = orc.round_to_fp16(rng.standard_normal(hkv * cap * d).astype(np.float32)).astype(np.float16)
@@ -253,7 +256,7 @@ def test_flash_attn_kvlen_graph_replay(orc, gpu):
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         P.flash_attn_decode(p, qd, kd, vd, out=o, lse=lse, workspace=ws, kv_len=n_dev)
-    for n in [513, 600, 767, 768, 1]:
+    for n in lengths:
         n_dev.fill_(n)
         g.replay()
         torch.cuda.synchronize()
