@@ -265,8 +265,36 @@ def measure_fa(torch, P, lib, timer, gen, ctxs):
                         "gbs": round(b / (med * 1e-6) / 1e9, 1), "frac": round(b / (med * 1e-6) / 1e9 / PEAK_GBS, 4)}
         log(f"[bench] FA decode ctx {ctx}: {med:.2f} us ({fa[str(ctx)]['gbs']} GB/s)")
         del caches
+    # A short visible length in a large cache (device-side length, plan made for the capacity): the kernels spread
+    # the visible keys over every planned split, so this should cost what the same length costs on its own.
+    cap, kvlen = 8192, {}
+    p = P.AttnParams(n_head_q=32, n_head_kv=8, seq_q=1, seq_kv=cap, d_qk=128, d_v=128, causal=True)
+    nsets = max(2, min(16, (600 << 20) // (2 * 8 * cap * 128 * 2)))
+    caches = [(torch.randn(8 * cap * 128, device=dev, generator=gen).half(),
+               torch.randn(8 * cap * 128, device=dev, generator=gen).half()) for _ in range(nsets)]
+    q = torch.randn(32 * 128, device=dev, generator=gen)
+    o = torch.empty(32 * 128, device=dev)
+    lse = torch.empty(32, device=dev)
+    fws = torch.empty(P.flash_attn_decode_workspace(p) // 4 + 4, device=dev)
+    n_dev = torch.zeros(1, dtype=torch.int32, device=dev)
+    for n in (640, 2048):
+        n_dev.fill_(n)
+
+        def call(i, s):
+            k, v = caches[i % len(caches)]
+            lib.p1x_flash_attn_decode_kvlen(C.byref(p), C.c_void_p(q.data_ptr()), C.c_void_p(k.data_ptr()),
+                                            C.c_void_p(v.data_ptr()), None, None, C.c_void_p(n_dev.data_ptr()),
+                                            C.c_void_p(o.data_ptr()), C.c_void_p(lse.data_ptr()),
+                                            C.c_void_p(fws.data_ptr()), fws.numel() * 4, s)
+
+        med, mn, _ = timer.period_us(call, n=32)
+        kvlen[str(n)] = {"us": round(med, 3), "min_us": round(mn, 3)}
+        log(f"[bench] FA decode, {n} visible keys in a cache of {cap}: {med:.2f} us")
+    del caches
     return {"config": "32 q heads / 8 kv heads, d 128, 1 query row, causal, fp16 K/V, fp32 o + lse; split-K pass "
-                      "+ LSE combine pass (2 launches, timed together)", "by_ctx": fa}
+                      "+ LSE combine pass (2 launches, timed together)", "by_ctx": fa,
+            "kvlen_cap8192": {"config": "p1x_flash_attn_decode_kvlen over a cache of 8192 rows with the visible "
+                                        "length on the device", "by_len": kvlen}}
 
 
 def measure_fa_quant(torch, P, lib, synth, timer, gen, ctxs, kv_type):
