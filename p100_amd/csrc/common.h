@@ -213,10 +213,15 @@ __device__ __forceinline__ float group_sum(float v, int width) {
 // theta = pos * theta_scale^p, (x0 cos - x1 sin, x0 sin + x1 cos) (ggml rope_yarn with no frequency scaling,
 // ggml-cpu/ops.cpp rope_f32 normal mode). The FMAs are spelled out so every kernel that rotates a pair (the
 // standalone RoPE + KV append, the q/k/v mat-vec's fused epilogue) produces the same bits.
-__device__ __forceinline__ float2 rope_pair(float x0, float x1, int pos, int p, float theta_scale) {
+__device__ __forceinline__ float2 rope_cs(int pos, int p, float theta_scale) {  // (cos, sin) of the pair's angle
     const float theta = float(pos) * powf(theta_scale, float(p));
-    const float c = cosf(theta), s = sinf(theta);
-    return make_float2(fmaf(x0, c, -(x1 * s)), fmaf(x0, s, x1 * c));
+    return make_float2(cosf(theta), sinf(theta));
+}
+__device__ __forceinline__ float2 rope_rotate(float x0, float x1, float2 cs) {
+    return make_float2(fmaf(x0, cs.x, -(x1 * cs.y)), fmaf(x0, cs.y, x1 * cs.x));
+}
+__device__ __forceinline__ float2 rope_pair(float x0, float x1, int pos, int p, float theta_scale) {
+    return rope_rotate(x0, x1, rope_cs(pos, p, theta_scale));
 }
 
 }  // namespace p1x

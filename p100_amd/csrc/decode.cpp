@@ -49,7 +49,7 @@ p1x_attn_params attn_params(const p1x_llama_hparams& hp) {
 
 // Workspace regions, each 256-byte aligned.
 struct Layout {
-    size_t x, y, qkv, qr, ao, gu, qs, ds, logits, fa, fa_bytes, argmax, total;
+    size_t x, y, qkv, qr, ao, gu, qs, ds, logits, fa, fa_bytes, argmax, rope, total;
 };
 Layout layout(const p1x_llama_hparams& hp) {
     Layout L{};
@@ -74,6 +74,7 @@ Layout layout(const p1x_llama_hparams& hp) {
     L.fa_bytes = fa_workspace(&ap);
     L.fa = take(L.fa_bytes);
     L.argmax = take(p1x::argmax_workspace(hp.n_vocab));
+    L.rope = take(d / 2 * 8);  // the step's RoPE (cos, sin) per pair index
     L.total = off;
     return L;
 }
@@ -219,7 +220,9 @@ int p1x_llama_decode_step(const p1x_llama_model* m, p1x_decode_state* state, con
     do {                                            \
         if ((e = (call)) != hipSuccess) return hip_fail(e, what); \
     } while (0)
-    P1X_TRY(p1x::launch_decode_embed(hp.embd_type, m->tok_embd, nb_e, hp.n_vocab, E, st, prompt, tokens, hp.n_ctx, x, s),
+    auto* rope_cs = reinterpret_cast<float2*>(base + W.rope);
+    P1X_TRY(p1x::launch_decode_embed(hp.embd_type, m->tok_embd, nb_e, hp.n_vocab, E, st, prompt, tokens, hp.n_ctx, x,
+                                     rope_fused ? rope_cs : nullptr, d / 2, theta_scale, s),
             "decode embed");
     for (int l = 0; l < hp.n_layer; ++l) {
         const p1x_llama_layer& L = m->layers[l];
@@ -228,7 +231,7 @@ int p1x_llama_decode_step(const p1x_llama_model* m, p1x_decode_state* state, con
         const auto* wq = static_cast<const uint8_t*>(L.wq);
         const bool stacked = L.wk == wq + E * nb_w && L.wv == wq + (E + kv) * nb_w;
         if (rope_fused) {  // the projection rotates q / k and appends k / v itself
-            p1x::RopeKv rk{qr, L.k_cache, L.v_cache, int(E), int(kv), d, hp.n_ctx, 0, &state->pos, theta_scale};
+            p1x::RopeKv rk{qr, L.k_cache, L.v_cache, int(E), int(kv), d, hp.n_ctx, 0, &state->pos, rope_cs};
             if (stacked) {
                 P1X_TRY(p1x::launch_mmvq_rope_kv(hp.wtype, wq, nb_w, E + 2 * kv, E, qs, ds, rk, s), "qkv + rope");
             } else {

@@ -23,12 +23,16 @@ template <int TYPE, bool DECODE>
 __global__ __launch_bounds__(256) void k_get_rows(const uint8_t* __restrict__ w, int64_t nb01, int n_rows, int K,
                                                   const int* __restrict__ row_dev, DecodeState* st,
                                                   const int* __restrict__ prompt, const int* __restrict__ tokens,
-                                                  int n_ctx, float* __restrict__ out) {
+                                                  int n_ctx, float* __restrict__ out, float2* __restrict__ cs_out,
+                                                  int half_d, float theta_scale) {
     int row;
     if constexpr (DECODE) {
         const int pos = st->pos;
         row = pos < 0 ? 0 : (pos < st->n_prompt ? prompt[pos] : (pos <= n_ctx ? tokens[pos] : 0));
         if (blockIdx.x == 0 && threadIdx.x == 0) st->n_kv = pos < 0 ? 0 : (pos + 1 < n_ctx ? pos + 1 : n_ctx);
+        // The step's RoPE angles, (cos, sin) of every pair index at this position, for the q/k/v projection.
+        if (cs_out && blockIdx.x == 0)
+            for (int p = threadIdx.x; p < half_d; p += 256) cs_out[p] = rope_cs(pos, p, theta_scale);
     } else {
         row = *row_dev;
     }
@@ -256,23 +260,24 @@ hipError_t launch_get_rows(int type, const void* w, int64_t nb01, int n_rows, in
     const auto* wb = static_cast<const uint8_t*>(w);
     if (type == Q4_0)
         hipLaunchKernelGGL((k_get_rows<Q4_0, false>), grid, dim3(256), 0, stream, wb, nb01, n_rows, K, row_dev,
-                           nullptr, nullptr, nullptr, 0, out);
+                           nullptr, nullptr, nullptr, 0, out, nullptr, 0, 0.0f);
     else
         hipLaunchKernelGGL((k_get_rows<Q8_0, false>), grid, dim3(256), 0, stream, wb, nb01, n_rows, K, row_dev,
-                           nullptr, nullptr, nullptr, 0, out);
+                           nullptr, nullptr, nullptr, 0, out, nullptr, 0, 0.0f);
     return hipGetLastError();
 }
 
 hipError_t launch_decode_embed(int type, const void* w, int64_t nb01, int n_rows, int K, DecodeState* st,
-                               const int* prompt, const int* tokens, int n_ctx, float* out, hipStream_t stream) {
+                               const int* prompt, const int* tokens, int n_ctx, float* out, float2* rope_cs,
+                               int half_d, float theta_scale, hipStream_t stream) {
     const dim3 grid((K + 255) / 256);
     const auto* wb = static_cast<const uint8_t*>(w);
     if (type == Q4_0)
         hipLaunchKernelGGL((k_get_rows<Q4_0, true>), grid, dim3(256), 0, stream, wb, nb01, n_rows, K, nullptr, st,
-                           prompt, tokens, n_ctx, out);
+                           prompt, tokens, n_ctx, out, rope_cs, half_d, theta_scale);
     else
         hipLaunchKernelGGL((k_get_rows<Q8_0, true>), grid, dim3(256), 0, stream, wb, nb01, n_rows, K, nullptr, st,
-                           prompt, tokens, n_ctx, out);
+                           prompt, tokens, n_ctx, out, rope_cs, half_d, theta_scale);
     return hipGetLastError();
 }
 

@@ -24,7 +24,7 @@ struct RopeKv {
     uint16_t *k_cache, *v_cache;
     int E, kv, d, n_ctx, row_base;
     const int* pos;
-    float theta_scale;
+    const float2* cs;  // (cos, sin) of pair indices 0 .. d/2-1 at *pos (launch_decode_embed writes them)
 };
 bool mmvq_rope_kv_supported(int type, int M, int K, int d);
 hipError_t launch_mmvq_rope_kv(int type, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
@@ -71,8 +71,10 @@ struct DecodeState {
 };
 hipError_t launch_get_rows(int type, const void* w, int64_t nb01, int n_rows, int K, const int* row_dev, float* out,
                            hipStream_t stream);
+// Also writes the step's RoPE (cos, sin) for pair indices 0 .. half_d-1 into rope_cs when it is not null.
 hipError_t launch_decode_embed(int type, const void* w, int64_t nb01, int n_rows, int K, DecodeState* st,
-                               const int* prompt, const int* tokens, int n_ctx, float* out, hipStream_t stream);
+                               const int* prompt, const int* tokens, int n_ctx, float* out, float2* rope_cs,
+                               int half_d, float theta_scale, hipStream_t stream);
 hipError_t launch_rms_norm_q8_1(float* x, const float* add, const float* w, int n, float eps, int8_t* qs, float* ds,
                                 float* h_out, hipStream_t stream);
 int rms_norm_max_n();

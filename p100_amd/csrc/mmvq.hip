@@ -454,27 +454,51 @@ __global__ __launch_bounds__(256) void k_mmvq_fx(const uint8_t* __restrict__ w, 
 // to unit 0 and dropped by a select; rows past M are clamped for the loads and never stored.
 // Epilogues of k_mmvr: the row sums stored as they are, or one token's q/k/v rows rotated in adjacent pairs and
 // appended to the KV cache (RopeKv; R is even there, so a row-group holds whole pairs).
+// An epilogue's `start` runs before the weight stream is requested (its own loads go first) and `prepare` once the
+// loads are in flight, so per-row-group set-up overlaps the memory latency instead of following the compute.
 struct EpiRows {
     static constexpr bool kPairs = false;
+    template <int NP>
+    struct State {};
     float* y;
+    __device__ __forceinline__ int start() const { return 0; }
+    template <int NP>
+    __device__ __forceinline__ State<NP> prepare(int, int) const { return {}; }
     __device__ __forceinline__ void row(int r, float v, int M) const {
         if (r < M) y[r] = v;
     }
 };
 struct EpiRopeKv {
     static constexpr bool kPairs = true;
+    template <int NP>
+    struct State {
+        int pos;
+        float2 cs[NP];  // (cos, sin) of pair j of the row-group (rows row0 + 2j, row0 + 2j + 1)
+    };
     RopeKv a;
-    __device__ __forceinline__ void pair(int r, float v0, float v1, int M) const {
+    __device__ __forceinline__ int start() const { return *a.pos; }
+    template <int NP>
+    __device__ __forceinline__ State<NP> prepare(int pos, int row0) const {
+        State<NP> st;
+        st.pos = pos;
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
+            const int g = a.row_base + row0 + 2 * j;
+            const int u = g < a.E ? g : g - a.E;  // q rows, then k rows (v rows are not rotated)
+            st.cs[j] = a.cs[(u % a.d) >> 1];
+        }
+        return st;
+    }
+    __device__ __forceinline__ void pair(int r, float2 cs, float v0, float v1, int M, int pos) const {
         if (r >= M) return;
-        const int g = a.row_base + r, pos = *a.pos;
+        const int g = a.row_base + r;
         const bool row_ok = pos >= 0 && pos < a.n_ctx;
         if (g < a.E) {
-            const int i = g % a.d;
-            *reinterpret_cast<float2*>(a.q_out + g) = rope_pair(v0, v1, pos, i >> 1, a.theta_scale);
+            *reinterpret_cast<float2*>(a.q_out + g) = rope_rotate(v0, v1, cs);
         } else if (row_ok) {
             const bool is_k = g < a.E + a.kv;
             const int u = g - a.E - (is_k ? 0 : a.kv), h = u / a.d, i = u - h * a.d;
-            const float2 o = is_k ? rope_pair(v0, v1, pos, i >> 1, a.theta_scale) : make_float2(v0, v1);
+            const float2 o = is_k ? rope_rotate(v0, v1, cs) : make_float2(v0, v1);
             __half* cache = reinterpret_cast<__half*>(is_k ? a.k_cache : a.v_cache);
             *reinterpret_cast<__half2*>(cache + (size_t(h) * a.n_ctx + pos) * a.d + i) = __floats2half2_rn(o.x, o.y);
         }
@@ -486,6 +510,7 @@ __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int
                                               const int8_t* __restrict__ xq, const float4* __restrict__ xds,
                                               const EPI epi, int32_t* __restrict__ gs) {
     static_assert(!EPI::kPairs || R % 2 == 0, "row pairs stay inside one row-group");
+    constexpr int NP = EPI::kPairs ? R / 2 : 1;
     using U = typename UnitOf<TYPE>::T;
     static_assert(U::kActBlocks == 1 && U::kGroups == 1, "one Q8_1 block and one int32 sum per unit");
     constexpr int T = 64 * NWK, G = 4 / NWK;
@@ -493,6 +518,7 @@ __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int
     const int tid = threadIdx.x, g = tid / T, t = tid - g * T;
     const int units = K / U::kElems;
     const int row0 = (blockIdx.x * G + g) * R;
+    const int epi_in = epi.start();
     const ActGlobal act{xq, xds, K};
     ActBlock x[UPT];
     int uc[UPT];
@@ -511,6 +537,7 @@ __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int
 #pragma unroll
         for (int j = 0; j < UPT; ++j) wv[r][j].load(wr, uc[j]);
     }
+    const auto est = epi.template prepare<NP>(epi_in, row0);
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -530,7 +557,7 @@ __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int
 #pragma unroll
             for (int r = 0; r < R; r += EPI::kPairs ? 2 : 1) {
                 if constexpr (EPI::kPairs)
-                    epi.pair(row0 + r, acc[r], acc[r + 1], M);
+                    epi.pair(row0 + r, est.cs[r / 2], acc[r], acc[r + 1], M, est.pos);
                 else
                     epi.row(row0 + r, acc[r], M);
             }
@@ -549,7 +576,10 @@ __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int
         }
         if constexpr (EPI::kPairs) {
             const float next = __shfl_down(sum, 1);  // every lane of the wave takes part
-            if (t < R && !(t & 1)) epi.pair(row0 + t, sum, next, M);
+            float2 cs = est.cs[0];                   // pair t / 2, selected without a lane-dependent index
+#pragma unroll
+            for (int j = 1; j < NP; ++j) cs = (t >> 1) == j ? est.cs[j] : cs;
+            if (t < R && !(t & 1)) epi.pair(row0 + t, cs, sum, next, M, est.pos);
         } else if (t < R) {
             epi.row(row0 + t, sum, M);
         }
