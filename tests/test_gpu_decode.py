@@ -450,6 +450,42 @@ def test_decode_graph_replay_matches_eager(gpu):
     assert g2 == e2
 
 
+@pytest.mark.parametrize("wtype", [2, 8])
+def test_decode_step_separate_projection_weights(gpu, wtype):
+    """Wq / Wk / Wv and gate / up in separate allocations (not back to back): the step runs one launch per matrix,
+    the q, k and v parts each with the fused RoPE + KV-append store step at its own row offset, and matches the
+    stacked layout exactly (tokens, logits, caches; K = 256 gives every matrix the same row-group shape)."""
+    import torch
+
+    from p100_amd import llama
+
+    stacked = tiny_model(wtype, wtype, 64, seed=11)
+    separate = tiny_model(wtype, wtype, 64, seed=11)  # the same weights, re-pointed below
+    hp = stacked.hp
+    E, F, kv = hp.n_embd, hp.n_ff, hp.n_head_kv * hp.head_dim
+    keep = []
+    for i, L in enumerate(separate.layers):
+        parts = [L["wqkv"][:E], L["wqkv"][E:E + kv], L["wqkv"][E + kv:], L["w_gate_up"][:F], L["w_gate_up"][F:]]
+        offs, off = [], 0
+        for t in parts:  # a 256-byte gap after every matrix, so no two are adjacent
+            offs.append(off)
+            off += (t.numel() + 511) // 256 * 256
+        buf = torch.zeros(off, dtype=torch.uint8, device="cuda")
+        for t, o in zip(parts, offs):
+            buf[o:o + t.numel()].copy_(t.reshape(-1))
+        keep.append(buf)
+        c = separate._layers_c[i]
+        c.wq, c.wk, c.wv, c.w_gate, c.w_up = (buf.data_ptr() + o for o in offs)
+    prompt = [3, 1, 4, 1, 5]
+    d1, d2 = llama.Decoder(stacked, max_prompt=len(prompt)), llama.Decoder(separate, max_prompt=len(prompt))
+    t1 = d1.generate(prompt, 12, use_graph=False)
+    t2 = d2.generate(prompt, 12, use_graph=False)
+    assert t1 == t2
+    assert torch.equal(d1.logits, d2.logits)
+    for L1, L2 in zip(stacked.layers, separate.layers):
+        assert torch.equal(L1["k_cache"], L2["k_cache"]) and torch.equal(L1["v_cache"], L2["v_cache"])
+
+
 def test_decode_step_rejects_bad_arguments(gpu):
     import ctypes as C
 
