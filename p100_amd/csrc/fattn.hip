@@ -455,19 +455,81 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v + __shfl_xor(v, 32);
 }
 
+// The value of lane ^ K (exact permutations): DPP inside 16-lane rows for K < 16 (xor 1 and 2 by quad_perm,
+// xor 4 = row_half_mirror then the quad reversed, xor 8 = row rotation by 8), ds_swizzle for 16, a shuffle for 32.
+template <int K>
+__device__ __forceinline__ float lane_xor(float v) {
+    if constexpr (K == 1) return dpp_f<kXor1>(v);
+    else if constexpr (K == 2) return dpp_f<kXor2>(v);
+    else if constexpr (K == 4) return dpp_f<0x1B>(dpp_f<kHalfMirror>(v));  // quad_perm(3,2,1,0) after the mirror
+    else if constexpr (K == 8) return dpp_f<kRor8>(v);
+    else if constexpr (K == 16)
+        return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+    else return __shfl_xor(v, K);
+}
+template <int K>
+__device__ __forceinline__ int lane_xor_i(int v) {
+    return __builtin_bit_cast(int, lane_xor<K>(__builtin_bit_cast(float, v)));
+}
+// Max / sum over the 64 lanes, the same value in every lane: DPP inside the 16-lane rows, the four row results by
+// readlane (no LDS crossbar round trips).
+__device__ __forceinline__ float wave_max_rl(float v) {
+    v = fmaxf(v, dpp_f<kXor1>(v));
+    v = fmaxf(v, dpp_f<kXor2>(v));
+    v = fmaxf(v, dpp_f<kHalfMirror>(v));
+    v = fmaxf(v, dpp_f<kMirror>(v));
+    const int b = __builtin_bit_cast(int, v);
+    return fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)),
+                       __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))),
+                 fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)),
+                       __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48))));
+}
+__device__ __forceinline__ float wave_sum_rl(float v) {
+    v += dpp_f<kXor1>(v);
+    v += dpp_f<kXor2>(v);
+    v += dpp_f<kHalfMirror>(v);
+    v += dpp_f<kMirror>(v);
+    const int b = __builtin_bit_cast(int, v);
+    return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))) +
+           (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48)));
+}
+
 // Q8_1 of an output row held CPL consecutive columns per lane (the combine's layout), for a mat-vec that takes the
 // attention output next: element e of a 32-block sits in lane bits log2(CPL).. and in-lane bits below, and the
 // block sum follows the reference's butterfly order (offsets 16 .. 1; q8_1_store's arithmetic otherwise).
+// One step of the butterfly over the 32 elements of a block held CPL per lane: element offset OFF is the lane
+// distance OFF / CPL when OFF >= CPL, else a distance inside the lane.
+template <int OFF, int CPL>
+__device__ __forceinline__ void q8_1_bfly(float (&t)[CPL], int& isum) {
+    if constexpr (OFF >= CPL) {
+        isum += lane_xor_i<OFF / CPL>(isum);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) t[c] += lane_xor<OFF / CPL>(t[c]);
+    } else {
+        float u[CPL];
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) u[c] = t[c] + t[c ^ OFF];
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) t[c] = u[c];
+    }
+}
 template <int CPL>
 __device__ __forceinline__ void q8_1_row(const float* v, size_t col0, int8_t* __restrict__ qs, float4* __restrict__ ds) {
+    static_assert(CPL == 1 || CPL == 2 || CPL == 4, "32-element blocks over 32, 16 or 8 lanes");
     float m = 0.0f, t[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
         m = fmaxf(m, fabsf(v[c]));
         t[c] = v[c];
     }
-#pragma unroll
-    for (int off = 16; off >= CPL; off >>= 1) m = fmaxf(m, __shfl_xor(m, off / CPL));
+    // The block's 32 / CPL lanes: lane distances 16 / CPL .. 1 (exact permutations, max is order-free).
+    if constexpr (CPL == 1) m = fmaxf(m, lane_xor<16>(m));
+    if constexpr (CPL <= 2) m = fmaxf(m, lane_xor<8>(m));
+    m = fmaxf(m, lane_xor<4>(m));
+    m = fmaxf(m, lane_xor<2>(m));
+    m = fmaxf(m, lane_xor<1>(m));
     const float d = m / 127.0f;
     int q[CPL], isum = 0;
 #pragma unroll
@@ -476,20 +538,11 @@ __device__ __forceinline__ void q8_1_row(const float* v, size_t col0, int8_t* __
         isum += q[c];
         qs[col0 + c] = static_cast<int8_t>(q[c]);
     }
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) {
-        if (off >= CPL) {
-            isum += __shfl_xor(isum, off / CPL);
-#pragma unroll
-            for (int c = 0; c < CPL; ++c) t[c] += __shfl_xor(t[c], off / CPL);
-        } else {
-            float u[CPL];
-#pragma unroll
-            for (int c = 0; c < CPL; ++c) u[c] = t[c] + t[c ^ off];
-#pragma unroll
-            for (int c = 0; c < CPL; ++c) t[c] = u[c];
-        }
-    }
+    q8_1_bfly<16, CPL>(t, isum);  // the reference's butterfly order: offsets 16, 8, 4, 2, 1
+    q8_1_bfly<8, CPL>(t, isum);
+    q8_1_bfly<4, CPL>(t, isum);
+    q8_1_bfly<2, CPL>(t, isum);
+    q8_1_bfly<1, CPL>(t, isum);
     if (col0 % 32 == 0) ds[col0 / 32] = make_float4(round_fp16(d), round_fp16(t[0]), static_cast<float>(isum), 0.0f);
 }
 
@@ -502,7 +555,6 @@ template <int D, int NH>
 __global__ __launch_bounds__(256) void k_fa_combine(FaArgs a, int rows) {
     constexpr int CPL = D / 64;  // columns per lane
     constexpr int kRound = 32;   // splits per round of loads
-    __shared__ float wsh[kCombineWaves][kMaxSplits];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row = blockIdx.x * kCombineWaves + wave;
     if (row >= rows) return;  // whole wave; nothing below synchronizes across waves
@@ -540,28 +592,28 @@ __global__ __launch_bounds__(256) void k_fa_combine(FaArgs a, int rows) {
     float mx = ml[0].x;
 #pragma unroll
     for (int k = 1; k < kMaxSplits / 64; ++k) mx = fmaxf(mx, ml[k].x);
-    mx = wave_max(mx);
-    float den = 0.0f;
+    mx = wave_max_rl(mx);
+    float den = 0.0f, wv[kMaxSplits / 64];  // weight of split lane + 64 k, held by that lane
 #pragma unroll
     for (int k = 0; k < kMaxSplits / 64; ++k) {
-        const int sp = lane + 64 * k;
-        const float wv = (ml[k].y == 0.0f || mx == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ml[k].x - mx);
-        if (sp < a.splits) wsh[wave][sp] = wv;
-        den = fmaf(wv, ml[k].y, den);
+        wv[k] = (ml[k].y == 0.0f || mx == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ml[k].x - mx);
+        den = fmaf(wv[k], ml[k].y, den);
     }
-    den = wave_sum(den);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // this wave's LDS weights before any lane reads them
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    den = wave_sum_rl(den);
 
     float acc[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c) acc[c] = 0.0f;
     for (int s0 = 0; s0 < a.splits; s0 += kRound) {
         if (s0 > 0) load_round(s0);
+        float wk = wv[0];  // the register holding splits s0 .. s0 + kRound - 1 (a wave-uniform choice)
+#pragma unroll
+        for (int k = 1; k < kMaxSplits / 64; ++k) wk = (s0 >> 6) == k ? wv[k] : wk;
 #pragma unroll
         for (int u = 0; u < kRound; ++u) {
-            const float ww = s0 + u < a.splits ? wsh[wave][s0 + u] : 0.0f;
+            const float ww = s0 + u < a.splits ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                     __builtin_bit_cast(int, wk), (s0 & 63) + u))
+                                               : 0.0f;
 #pragma unroll
             for (int c = 0; c < CPL; ++c) acc[c] = fmaf(ww, buf[u][c], acc[c]);
         }

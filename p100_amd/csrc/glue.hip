@@ -95,12 +95,13 @@ __global__ __launch_bounds__(kNormMaxThreads) void k_rms_norm_q8_1(float* __rest
                                                                   float* __restrict__ h_out) {
     __shared__ float part[kNormMaxThreads / kWave];
     const int t = threadIdx.x, nt = blockDim.x;
-    float v[kNormMaxPasses][8];
+    float v[kNormMaxPasses][8], wv[kNormMaxPasses][8];
     float ss = 0.0f;
 #pragma unroll
     for (int r = 0; r < kNormMaxPasses; ++r) {
         const int e0 = (r * nt + t) * 8;
         if (e0 < n) {
+            load8(w + e0, wv[r]);  // requested with x and add: one memory round trip for the whole kernel
             load8(x + e0, v[r]);
             if (add) {
                 float a[8];
@@ -123,10 +124,9 @@ __global__ __launch_bounds__(kNormMaxThreads) void k_rms_norm_q8_1(float* __rest
     for (int r = 0; r < kNormMaxPasses; ++r) {
         const int e0 = (r * nt + t) * 8;
         if (e0 < n) {  // whole quads: n % 32 == 0
-            float wv[8], hv[8];
-            load8(w + e0, wv);
+            float hv[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) hv[e] = (v[r][e] * scale) * wv[e];
+            for (int e = 0; e < 8; ++e) hv[e] = (v[r][e] * scale) * wv[r][e];
             if (h_out) store8(h_out + e0, hv);
             store_q8_1(q8_1_quad(hv), e0, qs, ds);
         }
