@@ -224,9 +224,15 @@ int p1x_llama_decode_step(const p1x_llama_model* m, p1x_decode_state* state, con
     P1X_TRY(p1x::launch_decode_embed(hp.embd_type, m->tok_embd, nb_e, hp.n_vocab, E, st, prompt, tokens, hp.n_ctx, x,
                                      rope_fused ? rope_cs : nullptr, d / 2, theta_scale, s),
             "decode embed");
+    // The o and down projections add their output to the residual stream x themselves when the register-resident
+    // mat-vec applies (the same addition as the norm's x += y); `pending` is the output still to be added by the
+    // next norm otherwise.
+    const bool o_resid = (wo_prepared || !wo_fused) && p1x::mmvq_residual_supported(hp.wtype, E, E);
+    const bool down_resid = p1x::mmvq_residual_supported(hp.wtype, E, F);
+    const float* pending = nullptr;
     for (int l = 0; l < hp.n_layer; ++l) {
         const p1x_llama_layer& L = m->layers[l];
-        P1X_TRY(p1x::launch_rms_norm_q8_1(x, l ? y : nullptr, L.attn_norm, E, hp.rms_eps, qs, ds, nullptr, s),
+        P1X_TRY(p1x::launch_rms_norm_q8_1(x, pending, L.attn_norm, E, hp.rms_eps, qs, ds, nullptr, s),
                 "attention norm");
         const auto* wq = static_cast<const uint8_t*>(L.wq);
         const bool stacked = L.wk == wq + E * nb_w && L.wv == wq + (E + kv) * nb_w;
@@ -257,15 +263,18 @@ int p1x_llama_decode_step(const p1x_llama_model* m, p1x_decode_state* state, con
         fa.k = reinterpret_cast<const __half*>(L.k_cache);
         fa.v = reinterpret_cast<const __half*>(L.v_cache);
         P1X_TRY(p1x::launch_fa_decode(fa, 1, d, s), "attention");
-        if (wo_prepared) {
-            P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, L.wo, nb_w, E, E, qs, ds, nullptr, y, nullptr, s), "o");
+        if (!wo_prepared && !wo_fused) P1X_TRY(p1x::launch_quantize_q8_1(ao, qs, ds, E, 1, s), "o quantize");
+        if (o_resid) {
+            P1X_TRY(p1x::launch_mmvq_residual(hp.wtype, L.wo, nb_w, E, E, qs, ds, x, s), "o + residual");
+            pending = nullptr;
         } else if (wo_fused) {
             P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, L.wo, nb_w, E, E, nullptr, nullptr, ao, y, nullptr, s), "o");
+            pending = y;
         } else {
-            P1X_TRY(p1x::launch_quantize_q8_1(ao, qs, ds, E, 1, s), "o quantize");
             P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, L.wo, nb_w, E, E, qs, ds, nullptr, y, nullptr, s), "o");
+            pending = y;
         }
-        P1X_TRY(p1x::launch_rms_norm_q8_1(x, y, L.ffn_norm, E, hp.rms_eps, qs, ds, nullptr, s), "ffn norm");
+        P1X_TRY(p1x::launch_rms_norm_q8_1(x, pending, L.ffn_norm, E, hp.rms_eps, qs, ds, nullptr, s), "ffn norm");
         const auto* wg = static_cast<const uint8_t*>(L.w_gate);
         if (L.w_up == wg + F * nb_w) {
             P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, wg, nb_w, 2 * F, E, qs, ds, nullptr, gu, nullptr, s), "gate/up");
@@ -274,9 +283,15 @@ int p1x_llama_decode_step(const p1x_llama_model* m, p1x_decode_state* state, con
             P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, L.w_up, nb_w, F, E, qs, ds, nullptr, gu + F, nullptr, s), "up");
         }
         P1X_TRY(p1x::launch_swiglu_q8_1(gu, gu + F, F, qs, ds, nullptr, s), "swiglu");
-        P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, L.w_down, nb_down, E, F, qs, ds, nullptr, y, nullptr, s), "down");
+        if (down_resid) {
+            P1X_TRY(p1x::launch_mmvq_residual(hp.wtype, L.w_down, nb_down, E, F, qs, ds, x, s), "down + residual");
+            pending = nullptr;
+        } else {
+            P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, L.w_down, nb_down, E, F, qs, ds, nullptr, y, nullptr, s), "down");
+            pending = y;
+        }
     }
-    P1X_TRY(p1x::launch_rms_norm_q8_1(x, y, m->output_norm, E, hp.rms_eps, qs, ds, nullptr, s), "output norm");
+    P1X_TRY(p1x::launch_rms_norm_q8_1(x, pending, m->output_norm, E, hp.rms_eps, qs, ds, nullptr, s), "output norm");
     P1X_TRY(p1x::launch_mmvq(hp.output_type, 1, m->output, nb_out, hp.n_vocab, E, qs, ds, nullptr, out, nullptr, s),
             "output");
     P1X_TRY(p1x::launch_argmax(out, hp.n_vocab, base + W.argmax, nullptr, st, tokens, hp.n_ctx, s), "argmax");

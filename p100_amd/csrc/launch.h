@@ -26,6 +26,11 @@ struct RopeKv {
     const int* pos;
     const float2* cs;  // (cos, sin) of pair indices 0 .. d/2-1 at *pos (launch_decode_embed writes them)
 };
+// One column, prepared Q8_1: y = W x added to the residual stream x_res in place (x_res[r] += y[r]), the RMSNorm's
+// residual addition done by the producing mat-vec.
+bool mmvq_residual_supported(int type, int M, int K);
+hipError_t launch_mmvq_residual(int type, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
+                                float* x_res, hipStream_t stream);
 bool mmvq_rope_kv_supported(int type, int M, int K, int d);
 hipError_t launch_mmvq_rope_kv(int type, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
                                const RopeKv& rk, hipStream_t stream);

@@ -456,16 +456,26 @@ __global__ __launch_bounds__(256) void k_mmvq_fx(const uint8_t* __restrict__ w, 
 // appended to the KV cache (RopeKv; R is even there, so a row-group holds whole pairs).
 // An epilogue's `start` runs before the weight stream is requested (its own loads go first) and `prepare` once the
 // loads are in flight, so per-row-group set-up overlaps the memory latency instead of following the compute.
+// Rows stored as they are (y[r] = v), or added to a residual stream in place (add == y: y[r] = y[r] + v, the same
+// addition as the RMSNorm kernel's x += add); the residual rows of a row-group are requested with the weights.
 struct EpiRows {
     static constexpr bool kPairs = false;
-    template <int NP>
-    struct State {};
+    template <int R>
+    struct State {
+        float base[R];
+    };
     float* y;
+    const float* add;
     __device__ __forceinline__ int start() const { return 0; }
-    template <int NP>
-    __device__ __forceinline__ State<NP> prepare(int, int) const { return {}; }
-    __device__ __forceinline__ void row(int r, float v, int M) const {
-        if (r < M) y[r] = v;
+    template <int R>
+    __device__ __forceinline__ State<R> prepare(int, int row0, int M) const {
+        State<R> st;
+#pragma unroll
+        for (int j = 0; j < R; ++j) st.base[j] = add ? add[min(row0 + j, M - 1)] : 0.0f;
+        return st;
+    }
+    __device__ __forceinline__ void row(int r, float base, float v, int M) const {
+        if (r < M) y[r] = add ? base + v : v;
     }
 };
 struct EpiRopeKv {
@@ -477,8 +487,8 @@ struct EpiRopeKv {
     };
     RopeKv a;
     __device__ __forceinline__ int start() const { return *a.pos; }
-    template <int NP>
-    __device__ __forceinline__ State<NP> prepare(int pos, int row0) const {
+    template <int R, int NP = R / 2>
+    __device__ __forceinline__ State<NP> prepare(int pos, int row0, int) const {
         State<NP> st;
         st.pos = pos;
 #pragma unroll
@@ -510,7 +520,7 @@ __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int
                                               const int8_t* __restrict__ xq, const float4* __restrict__ xds,
                                               const EPI epi, int32_t* __restrict__ gs) {
     static_assert(!EPI::kPairs || R % 2 == 0, "row pairs stay inside one row-group");
-    constexpr int NP = EPI::kPairs ? R / 2 : 1;
+
     using U = typename UnitOf<TYPE>::T;
     static_assert(U::kActBlocks == 1 && U::kGroups == 1, "one Q8_1 block and one int32 sum per unit");
     constexpr int T = 64 * NWK, G = 4 / NWK;
@@ -537,7 +547,7 @@ __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int
 #pragma unroll
         for (int j = 0; j < UPT; ++j) wv[r][j].load(wr, uc[j]);
     }
-    const auto est = epi.template prepare<NP>(epi_in, row0);
+    const auto est = epi.template prepare<R>(epi_in, row0, M);
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -559,7 +569,7 @@ __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int
                 if constexpr (EPI::kPairs)
                     epi.pair(row0 + r, est.cs[r / 2], acc[r], acc[r + 1], M, est.pos);
                 else
-                    epi.row(row0 + r, acc[r], M);
+                    epi.row(row0 + r, est.base[r], acc[r], M);
             }
         }
     } else {
@@ -578,10 +588,13 @@ __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int
             const float next = __shfl_down(sum, 1);  // every lane of the wave takes part
             float2 cs = est.cs[0];                   // pair t / 2, selected without a lane-dependent index
 #pragma unroll
-            for (int j = 1; j < NP; ++j) cs = (t >> 1) == j ? est.cs[j] : cs;
+            for (int j = 1; j < R / 2; ++j) cs = (t >> 1) == j ? est.cs[j] : cs;
             if (t < R && !(t & 1)) epi.pair(row0 + t, cs, sum, next, M, est.pos);
-        } else if (t < R) {
-            epi.row(row0 + t, sum, M);
+        } else {
+            float base = est.base[0];  // row t's residual value, selected without a lane-dependent index
+#pragma unroll
+            for (int j = 1; j < R; ++j) base = t == j ? est.base[j] : base;
+            if (t < R) epi.row(row0 + t, base, sum, M);
         }
     }
 }
@@ -713,8 +726,8 @@ hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int 
     const auto* d4 = reinterpret_cast<const float4*>(xds);
     MmvrPlan plan;
     if (B == 1 && !x && P1X_MMVR_ENABLE && (type == Q4_0 || type == Q8_0) && mmvr_plan(type, M, K, plan))
-        return type == Q4_0 ? launch_mmvr<Q4_0>(plan, wb, nb01, M, K, xq, d4, EpiRows{y}, gs, stream)
-                            : launch_mmvr<Q8_0>(plan, wb, nb01, M, K, xq, d4, EpiRows{y}, gs, stream);
+        return type == Q4_0 ? launch_mmvr<Q4_0>(plan, wb, nb01, M, K, xq, d4, EpiRows{y, nullptr}, gs, stream)
+                            : launch_mmvr<Q8_0>(plan, wb, nb01, M, K, xq, d4, EpiRows{y, nullptr}, gs, stream);
     switch (type) {
         case Q4_0: return launch_type<Q4_0>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
         case Q8_0: return launch_type<Q8_0>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
@@ -722,6 +735,21 @@ hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int 
         case Q6_K: return launch_type<Q6_K>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
     }
     return hipErrorInvalidValue;
+}
+
+bool mmvq_residual_supported(int type, int M, int K) {
+    MmvrPlan plan;
+    return P1X_MMVR_ENABLE && (type == Q4_0 || type == Q8_0) && mmvr_plan(type, M, K, plan);
+}
+
+hipError_t launch_mmvq_residual(int type, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
+                                float* x, hipStream_t stream) {
+    MmvrPlan plan;
+    if (!mmvq_residual_supported(type, M, K) || !mmvr_plan(type, M, K, plan)) return hipErrorInvalidValue;
+    const auto* wb = static_cast<const uint8_t*>(w);
+    const auto* d4 = reinterpret_cast<const float4*>(xds);
+    return type == Q4_0 ? launch_mmvr<Q4_0>(plan, wb, nb01, M, K, xq, d4, EpiRows{x, x}, nullptr, stream)
+                        : launch_mmvr<Q8_0>(plan, wb, nb01, M, K, xq, d4, EpiRows{x, x}, nullptr, stream);
 }
 
 bool mmvq_rope_kv_supported(int type, int M, int K, int d) {
