@@ -213,6 +213,9 @@ __device__ __forceinline__ float group_sum(float v, int width) {
 // theta = pos * theta_scale^p, (x0 cos - x1 sin, x0 sin + x1 cos) (ggml rope_yarn with no frequency scaling,
 // ggml-cpu/ops.cpp rope_f32 normal mode). The FMAs are spelled out so every kernel that rotates a pair (the
 // standalone RoPE + KV append, the q/k/v mat-vec's fused epilogue) produces the same bits.
+// ggml's swiglu: silu(g) * u with silu(g) = g / (1 + exp(-g)), shared by every kernel that computes it.
+__device__ __forceinline__ float swiglu(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
 __device__ __forceinline__ float2 rope_cs(int pos, int p, float theta_scale) {  // (cos, sin) of the pair's angle
     const float theta = float(pos) * powf(theta_scale, float(p));
     return make_float2(cosf(theta), sinf(theta));

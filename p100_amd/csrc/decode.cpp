@@ -229,6 +229,7 @@ int p1x_llama_decode_step(const p1x_llama_model* m, p1x_decode_state* state, con
     // next norm otherwise.
     const bool o_resid = (wo_prepared || !wo_fused) && p1x::mmvq_residual_supported(hp.wtype, E, E);
     const bool down_resid = p1x::mmvq_residual_supported(hp.wtype, E, F);
+    const bool swiglu_fused = p1x::mmvq_residual_supported(hp.wtype, 2 * F, E);
     const float* pending = nullptr;
     for (int l = 0; l < hp.n_layer; ++l) {
         const p1x_llama_layer& L = m->layers[l];
@@ -276,13 +277,18 @@ int p1x_llama_decode_step(const p1x_llama_model* m, p1x_decode_state* state, con
         }
         P1X_TRY(p1x::launch_rms_norm_q8_1(x, pending, L.ffn_norm, E, hp.rms_eps, qs, ds, nullptr, s), "ffn norm");
         const auto* wg = static_cast<const uint8_t*>(L.w_gate);
-        if (L.w_up == wg + F * nb_w) {
-            P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, wg, nb_w, 2 * F, E, qs, ds, nullptr, gu, nullptr, s), "gate/up");
+        if (L.w_up == wg + F * nb_w && swiglu_fused) {  // the mat-vec writes silu(gate) * up; then its Q8_1
+            P1X_TRY(p1x::launch_mmvq_swiglu(hp.wtype, wg, nb_w, F, E, qs, ds, gu, s), "gate/up + swiglu");
+            P1X_TRY(p1x::launch_quantize_q8_1(gu, qs, ds, F, 1, s), "swiglu quantize");
         } else {
-            P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, L.w_gate, nb_w, F, E, qs, ds, nullptr, gu, nullptr, s), "gate");
-            P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, L.w_up, nb_w, F, E, qs, ds, nullptr, gu + F, nullptr, s), "up");
+            if (L.w_up == wg + F * nb_w) {
+                P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, wg, nb_w, 2 * F, E, qs, ds, nullptr, gu, nullptr, s), "gate/up");
+            } else {
+                P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, L.w_gate, nb_w, F, E, qs, ds, nullptr, gu, nullptr, s), "gate");
+                P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, L.w_up, nb_w, F, E, qs, ds, nullptr, gu + F, nullptr, s), "up");
+            }
+            P1X_TRY(p1x::launch_swiglu_q8_1(gu, gu + F, F, qs, ds, nullptr, s), "swiglu");
         }
-        P1X_TRY(p1x::launch_swiglu_q8_1(gu, gu + F, F, qs, ds, nullptr, s), "swiglu");
         if (down_resid) {
             P1X_TRY(p1x::launch_mmvq_residual(hp.wtype, L.w_down, nb_down, E, F, qs, ds, x, s), "down + residual");
             pending = nullptr;

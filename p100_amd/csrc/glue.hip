@@ -145,7 +145,7 @@ __global__ __launch_bounds__(256) void k_swiglu_q8_1(const float* __restrict__ g
     load8(gate + e0, g);
     load8(up + e0, u);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) hv[e] = g[e] / (1.0f + expf(-g[e])) * u[e];
+    for (int e = 0; e < 8; ++e) hv[e] = swiglu(g[e], u[e]);
     if (h_out) store8(h_out + e0, hv);
     store_q8_1(q8_1_quad(hv), e0, qs, ds);
 }

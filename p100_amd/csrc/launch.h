@@ -31,6 +31,11 @@ struct RopeKv {
 bool mmvq_residual_supported(int type, int M, int K);
 hipError_t launch_mmvq_residual(int type, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
                                 float* x_res, hipStream_t stream);
+// One column, prepared Q8_1, gate rows [0, F) and up rows [F, 2F) stacked with row stride nb01: h[i] = silu(gate_i . x)
+// * (up_i . x), the mat-vec writing SwiGLU's output instead of both rows (supported where mmvq_residual_supported
+// holds for 2F rows).
+hipError_t launch_mmvq_swiglu(int type, const void* w, int64_t nb01, int F, int K, const int8_t* xq, const float* xds,
+                              float* h, hipStream_t stream);
 bool mmvq_rope_kv_supported(int type, int M, int K, int d);
 hipError_t launch_mmvq_rope_kv(int type, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
                                const RopeKv& rk, hipStream_t stream);

@@ -466,6 +466,7 @@ struct EpiRows {
     };
     float* y;
     const float* add;
+    __device__ __forceinline__ int phys_row(int r) const { return r; }
     __device__ __forceinline__ int start() const { return 0; }
     template <int R>
     __device__ __forceinline__ State<R> prepare(int, int row0, int M) const {
@@ -485,8 +486,20 @@ struct EpiRopeKv {
         int pos;
         float2 cs[NP];  // (cos, sin) of pair j of the row-group (rows row0 + 2j, row0 + 2j + 1)
     };
+    struct Param {
+        float2 cs;
+        int pos;
+    };
     RopeKv a;
+    __device__ __forceinline__ int phys_row(int r) const { return r; }
     __device__ __forceinline__ int start() const { return *a.pos; }
+    template <int R>
+    __device__ __forceinline__ Param param(const State<R / 2>& st, int j) const {  // pair j, no dynamic index
+        float2 cs = st.cs[0];
+#pragma unroll
+        for (int k = 1; k < R / 2; ++k) cs = j == k ? st.cs[k] : cs;
+        return {cs, st.pos};
+    }
     template <int R, int NP = R / 2>
     __device__ __forceinline__ State<NP> prepare(int pos, int row0, int) const {
         State<NP> st;
@@ -499,9 +512,10 @@ struct EpiRopeKv {
         }
         return st;
     }
-    __device__ __forceinline__ void pair(int r, float2 cs, float v0, float v1, int M, int pos) const {
+    __device__ __forceinline__ void pair(int r, const Param& p, float v0, float v1, int M) const {
         if (r >= M) return;
-        const int g = a.row_base + r;
+        const int g = a.row_base + r, pos = p.pos;
+        const float2 cs = p.cs;
         const bool row_ok = pos >= 0 && pos < a.n_ctx;
         if (g < a.E) {
             *reinterpret_cast<float2*>(a.q_out + g) = rope_rotate(v0, v1, cs);
@@ -512,6 +526,27 @@ struct EpiRopeKv {
             __half* cache = reinterpret_cast<__half*>(is_k ? a.k_cache : a.v_cache);
             *reinterpret_cast<__half2*>(cache + (size_t(h) * a.n_ctx + pos) * a.d + i) = __floats2half2_rn(o.x, o.y);
         }
+    }
+};
+
+// SwiGLU of the stacked gate / up matrix: logical row 2i is gate row i and 2i + 1 is up row i (physical rows i and
+// F + i), so a row-group holds whole pairs and its store step writes h[i] = silu(gate) * up (the arithmetic of
+// k_swiglu_q8_1) instead of both rows.
+struct EpiSwiGLU {
+    static constexpr bool kPairs = true;
+    template <int NP>
+    struct State {};
+    struct Param {};
+    float* h;
+    int F;
+    __device__ __forceinline__ int phys_row(int r) const { return (r & 1) ? F + (r >> 1) : (r >> 1); }
+    __device__ __forceinline__ int start() const { return 0; }
+    template <int R, int NP = R / 2>
+    __device__ __forceinline__ State<NP> prepare(int, int, int) const { return {}; }
+    template <int R>
+    __device__ __forceinline__ Param param(const State<R / 2>&, int) const { return {}; }
+    __device__ __forceinline__ void pair(int r, const Param&, float g, float u, int M) const {
+        if (r < M) h[r >> 1] = swiglu(g, u);
     }
 };
 
@@ -543,7 +578,7 @@ __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int
     U wv[R][UPT];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const uint8_t* wr = w + size_t(min(row0 + r, M - 1)) * nb01;
+        const uint8_t* wr = w + size_t(epi.phys_row(min(row0 + r, M - 1))) * nb01;
 #pragma unroll
         for (int j = 0; j < UPT; ++j) wv[r][j].load(wr, uc[j]);
     }
@@ -567,7 +602,7 @@ __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int
 #pragma unroll
             for (int r = 0; r < R; r += EPI::kPairs ? 2 : 1) {
                 if constexpr (EPI::kPairs)
-                    epi.pair(row0 + r, est.cs[r / 2], acc[r], acc[r + 1], M, est.pos);
+                    epi.pair(row0 + r, epi.template param<R>(est, r / 2), acc[r], acc[r + 1], M);
                 else
                     epi.row(row0 + r, est.base[r], acc[r], M);
             }
@@ -586,10 +621,7 @@ __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int
         }
         if constexpr (EPI::kPairs) {
             const float next = __shfl_down(sum, 1);  // every lane of the wave takes part
-            float2 cs = est.cs[0];                   // pair t / 2, selected without a lane-dependent index
-#pragma unroll
-            for (int j = 1; j < R / 2; ++j) cs = (t >> 1) == j ? est.cs[j] : cs;
-            if (t < R && !(t & 1)) epi.pair(row0 + t, cs, sum, next, M, est.pos);
+            if (t < R && !(t & 1)) epi.pair(row0 + t, epi.template param<R>(est, t >> 1), sum, next, M);
         } else {
             float base = est.base[0];  // row t's residual value, selected without a lane-dependent index
 #pragma unroll
@@ -750,6 +782,17 @@ hipError_t launch_mmvq_residual(int type, const void* w, int64_t nb01, int M, in
     const auto* d4 = reinterpret_cast<const float4*>(xds);
     return type == Q4_0 ? launch_mmvr<Q4_0>(plan, wb, nb01, M, K, xq, d4, EpiRows{x, x}, nullptr, stream)
                         : launch_mmvr<Q8_0>(plan, wb, nb01, M, K, xq, d4, EpiRows{x, x}, nullptr, stream);
+}
+
+hipError_t launch_mmvq_swiglu(int type, const void* w, int64_t nb01, int F, int K, const int8_t* xq, const float* xds,
+                              float* h, hipStream_t stream) {
+    MmvrPlan plan;
+    if (!mmvq_residual_supported(type, 2 * F, K) || !mmvr_plan(type, 2 * F, K, plan)) return hipErrorInvalidValue;
+    if (plan.r == 1) plan.r = 2;  // the same per-row arithmetic, whole (gate, up) pairs per row-group
+    const auto* wb = static_cast<const uint8_t*>(w);
+    const auto* d4 = reinterpret_cast<const float4*>(xds);
+    return type == Q4_0 ? launch_mmvr<Q4_0>(plan, wb, nb01, 2 * F, K, xq, d4, EpiSwiGLU{h, F}, nullptr, stream)
+                        : launch_mmvr<Q8_0>(plan, wb, nb01, 2 * F, K, xq, d4, EpiSwiGLU{h, F}, nullptr, stream);
 }
 
 bool mmvq_rope_kv_supported(int type, int M, int K, int d) {
