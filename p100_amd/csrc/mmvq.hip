@@ -681,6 +681,124 @@ hipError_t launch_mmvr(const MmvrPlan& p, const uint8_t* w, int64_t nb01, int M,
     return hipErrorInvalidValue;
 }
 
+// 2..4 activation columns (q4_0 / q8_0, prepared Q8_1): k_mmvr with B columns. Each thread holds its units' Q8_1
+// blocks of every column (B x UPT blocks) and each decoded weight unit serves the B columns; rows are stored as
+// they are (y[c][r]).
+template <int TYPE, int NWK, int UPT, int R, int B, bool SUMS>
+__global__ __launch_bounds__(256) void k_mmvr_cols(const uint8_t* __restrict__ w, int64_t nb01, int M, int K,
+                                                   const int8_t* __restrict__ xq, const float4* __restrict__ xds,
+                                                   float* __restrict__ y, int32_t* __restrict__ gs) {
+    using U = typename UnitOf<TYPE>::T;
+    static_assert(U::kActBlocks == 1 && U::kGroups == 1, "one Q8_1 block and one int32 sum per unit");
+    constexpr int T = 64 * NWK, G = 4 / NWK;
+    __shared__ float red[4][R * B];
+    const int tid = threadIdx.x, g = tid / T, t = tid - g * T;
+    const int units = K / U::kElems;
+    const int row0 = (blockIdx.x * G + g) * R;
+    const ActGlobal act{xq, xds, K};
+    ActBlock x[UPT][B];
+    int uc[UPT];
+    bool uok[UPT];
+#pragma unroll
+    for (int j = 0; j < UPT; ++j) {
+        const int u = t + T * j;
+        uok[j] = u < units;
+        uc[j] = uok[j] ? u : 0;
+#pragma unroll
+        for (int c = 0; c < B; ++c) x[j][c] = act.get(c, uc[j]);
+    }
+    U wv[R][UPT];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint8_t* wr = w + size_t(min(row0 + r, M - 1)) * nb01;
+#pragma unroll
+        for (int j = 0; j < UPT; ++j) wv[r][j].load(wr, uc[j]);
+    }
+    float acc[R][B];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int c = 0; c < B; ++c) {
+            float a = 0.0f;
+#pragma unroll
+            for (int j = 0; j < UPT; ++j) {
+                int32_t gg[1];
+                const float v = wv[r][j].acc(&x[j][c], a, gg);
+                a = uok[j] ? v : a;
+                if (SUMS && uok[j] && row0 + r < M) gs[(size_t(c) * M + row0 + r) * units + t + T * j] = gg[0];
+            }
+            acc[r][c] = wave_total(a);
+        }
+    const int lane = tid & 63;
+    if constexpr (NWK == 1) {
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int c = 0; c < B; ++c)
+                    if (row0 + r < M) y[size_t(c) * M + row0 + r] = acc[r][c];
+        }
+    } else {
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int c = 0; c < B; ++c) red[tid >> 6][r * B + c] = acc[r][c];
+        }
+        __syncthreads();
+        if (t < R * B) {
+            const int r = t / B, c = t - r * B;
+            float sum = red[g * NWK][t];
+#pragma unroll
+            for (int k = 1; k < NWK; ++k) sum += red[g * NWK + k][t];
+            if (row0 + r < M) y[size_t(c) * M + row0 + r] = sum;
+        }
+    }
+}
+
+// Row-group shape of k_mmvr_cols (measured on the Llama-3-8B matrices at 2..4 columns against k_mmvq): rows of up
+// to 128 units take 2 waves x 1 unit x 2 rows where that is faster (M <= 4096, 2 columns, or q4_0 at 3 columns);
+// up to 256 units 2 x 2 x 2; up to 512 units 4 x 2 x 4 (4 x 2 x 2 for q4_0 at 2 columns). Otherwise k_mmvq.
+bool mmvr_cols_plan(int type, int M, int K, int B, MmvrPlan& p) {
+    if (!P1X_MMVR_ENABLE || (type != Q4_0 && type != Q8_0) || B < 2 || B > 4) return false;
+    const int units = K / 32;
+    if (units <= 128) {
+        if (!(M <= 4096 || B == 2 || (type == Q4_0 && B == 3))) return false;
+        p = {2, 1, 2};
+    } else if (units <= 256) {
+        p = {2, 2, 2};
+    } else if (units <= 512) {
+        p = (type == Q4_0 && B == 2) ? MmvrPlan{4, 2, 2} : MmvrPlan{4, 2, 4};
+    } else {
+        return false;
+    }
+    return true;
+}
+
+template <int TYPE>
+hipError_t launch_mmvr_cols(const MmvrPlan& p, int B, const uint8_t* w, int64_t nb01, int M, int K, const int8_t* xq,
+                            const float4* xds, float* y, int32_t* gs, hipStream_t stream) {
+#define P1X_COLS(NW, UP, RR, BB)                                                                                     \
+    if (p.nwk == NW && p.upt == UP && p.r == RR && B == BB) {                                                       \
+        const dim3 grid((M + (4 / NW) * RR - 1) / ((4 / NW) * RR));                                                 \
+        if (gs)                                                                                                     \
+            hipLaunchKernelGGL((k_mmvr_cols<TYPE, NW, UP, RR, BB, true>), grid, dim3(256), 0, stream, w, nb01, M, K, xq, \
+                               xds, y, gs);                                                                         \
+        else                                                                                                        \
+            hipLaunchKernelGGL((k_mmvr_cols<TYPE, NW, UP, RR, BB, false>), grid, dim3(256), 0, stream, w, nb01, M, K,   \
+                               xq, xds, y, gs);                                                                     \
+        return hipGetLastError();                                                                                   \
+    }
+#define P1X_COLS_B(NW, UP, RR) P1X_COLS(NW, UP, RR, 2) P1X_COLS(NW, UP, RR, 3) P1X_COLS(NW, UP, RR, 4)
+    P1X_COLS_B(2, 1, 2)
+    P1X_COLS_B(2, 2, 2)
+    P1X_COLS_B(4, 2, 2)
+    P1X_COLS_B(4, 2, 4)
+#undef P1X_COLS_B
+#undef P1X_COLS
+    return hipErrorInvalidValue;
+}
+
 template <int TYPE, int B>
 hipError_t launch_b(const uint8_t* w, int64_t nb01, int M, int K, int rw, const int8_t* xq, const float4* xds,
                     const float* x, float* y, int32_t* gs, hipStream_t stream) {
@@ -757,6 +875,9 @@ hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int 
     const auto* wb = static_cast<const uint8_t*>(w);
     const auto* d4 = reinterpret_cast<const float4*>(xds);
     MmvrPlan plan;
+    if (!x && mmvr_cols_plan(type, M, K, B, plan))
+        return type == Q4_0 ? launch_mmvr_cols<Q4_0>(plan, B, wb, nb01, M, K, xq, d4, y, gs, stream)
+                            : launch_mmvr_cols<Q8_0>(plan, B, wb, nb01, M, K, xq, d4, y, gs, stream);
     if (B == 1 && !x && P1X_MMVR_ENABLE && (type == Q4_0 || type == Q8_0) && mmvr_plan(type, M, K, plan))
         return type == Q4_0 ? launch_mmvr<Q4_0>(plan, wb, nb01, M, K, xq, d4, EpiRows{y, nullptr}, gs, stream)
                             : launch_mmvr<Q8_0>(plan, wb, nb01, M, K, xq, d4, EpiRows{y, nullptr}, gs, stream);

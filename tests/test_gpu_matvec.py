@@ -246,6 +246,34 @@ def test_one_column_register_kernel(orc, gpu, tname):
             assert (y3.view(np.uint32) == y2.view(np.uint32)).all(), (rows, k)
 
 
+COLUMN_REGISTER_CASES = [(17, 2048), (1029, 4096), (4099, 4096), (37, 6144), (41, 8192), (45, 14336),
+                         (43, 16384), (19, 16416)]
+
+
+@pytest.mark.parametrize("ncols", [2, 3, 4])
+@pytest.mark.parametrize("tname", ["q4_0", "q8_0"])
+def test_column_register_kernel(orc, gpu, tname, ncols):
+    """2..4 columns on a prepared Q8_1 activation (the register-resident kernel where its plan applies, the
+    streaming kernel elsewhere): int32 group sums bit-exact per column, FP32 within the bars, the group-sum export
+    leaving the FP32 result unchanged, and a padded row stride."""
+    import p100_amd as P
+
+    t = orc.TYPES[tname]
+    for rows, k in COLUMN_REGISTER_CASES:
+        w, x = make_case(orc, t, k, rows, ncols, seed=32000 + 7 * ncols + rows + k)
+        q = P.quantize_q8_1(to_dev(x))
+        y, sums = P.mul_mat_vec(t, to_dev(w), rows, k, q, group_sums=True)
+        check_matvec(orc, t, w, x, y.cpu().numpy(), sums.cpu().numpy(), "q81")
+        y2 = P.mul_mat_vec(t, to_dev(w), rows, k, q).cpu().numpy()
+        assert (y2.view(np.uint32) == y.cpu().numpy().view(np.uint32)).all(), (rows, k)
+        if rows in (1029, 45):
+            rb = w.shape[1]
+            pad = np.zeros((rows, rb + 6), np.uint8)
+            pad[:, :rb] = w
+            y3 = P.mul_mat_vec(t, to_dev(pad), rows, k, q, nb01=rb + 6).cpu().numpy()
+            assert (y3.view(np.uint32) == y2.view(np.uint32)).all(), (rows, k)
+
+
 @pytest.mark.parametrize("tname", TYPES)
 def test_row_stride_and_large_m(orc, gpu, tname):
     """Padded row stride (nb01 > row bytes), and enough rows to use every work-group shape."""
