@@ -36,6 +36,9 @@
  *   p1x_get_rows             GGML_OP_GET_ROWS (token embedding), q4_0 / q8_0 rows
  *   p1x_rms_norm_q8_1        GGML_OP_ADD (residual) + GGML_OP_RMS_NORM + GGML_OP_MUL, emitting the Q8_1
  *                            activation of the next GGML_OP_MUL_MAT
+ *   p1x_rms_norm_mul_mat_vec GGML_OP_RMS_NORM + GGML_OP_MUL + GGML_OP_MUL_MAT (q4_0 / q8_0, ne11 = 1) in one
+ *                            launch: the mat-vec quantizes the normed vector itself (the two-op form is
+ *                            p1x_rms_norm_q8_1 then p1x_mul_mat_vec_q8_1)
  *   p1x_swiglu_q8_1          GGML_OP_GLU (swiglu), emitting the Q8_1 activation of the down projection
  *   p1x_rope_kv_append       GGML_OP_ROPE (normal mode) of q and k + GGML_OP_SET_ROWS of k and v into the cache
  *   p1x_argmax               GGML_OP_ARGMAX (greedy sampling)
@@ -173,6 +176,13 @@ int p1x_get_rows(int wtype, const void* w, int64_t nb01, int64_t n_rows, int64_t
  * h_out (f32 [n]) optional. n % 32 == 0, n <= 16384; every pointer 16-byte aligned. */
 int p1x_rms_norm_q8_1(float* x, const float* add, const float* w, int64_t n, float eps, int8_t* qs, float* ds,
                       float* h_out, void* stream);
+
+/* y[r] = sum_k w[r][k] * h[k] for h the Q8_1 activation of (x * rsqrt(mean(x^2) + eps)) * norm_w: the result of
+ * p1x_rms_norm_q8_1 (no add) followed by p1x_mul_mat_vec_q8_1 on one column, bit for bit, in one launch. Every
+ * work-group normalizes and quantizes x itself. wtype q4_0 or q8_0; K % 32 == 0, K <= 8192; x and norm_w 16-byte
+ * aligned; y f32 [M]. */
+int p1x_rms_norm_mul_mat_vec(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K, const float* x,
+                             const float* norm_w, float eps, float* y, void* stream);
 
 /* h = silu(gate) * up with silu(g) = g / (1 + exp(-g)), and its Q8_1 activation; h_out optional. n % 32 == 0;
  * every pointer 16-byte aligned. */

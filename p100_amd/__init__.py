@@ -33,7 +33,8 @@ OK, EINVAL, EUNSUPPORTED, EHIP, EWORKSPACE = 0, 1, 2, 3, 4
 EXPORTS = ["p1x_version", "p1x_init", "p1x_last_error", "p1x_quantize_q8_1", "p1x_prepare_h16",
            "p1x_mul_mat_vec_workspace", "p1x_mul_mat_vec", "p1x_mul_mat_vec_q8_1", "p1x_mul_mat_vec_h16",
            "p1x_attn_validate", "p1x_flash_attn_decode_workspace", "p1x_flash_attn_decode",
-           "p1x_flash_attn_decode_kvlen", "p1x_round_to_fp16", "p1x_get_rows", "p1x_rms_norm_q8_1", "p1x_swiglu_q8_1",
+           "p1x_flash_attn_decode_kvlen", "p1x_round_to_fp16", "p1x_get_rows", "p1x_rms_norm_q8_1", "p1x_rms_norm_mul_mat_vec",
+           "p1x_swiglu_q8_1",
            "p1x_rope_kv_append", "p1x_argmax_workspace", "p1x_argmax", "p1x_llama_workspace", "p1x_llama_decode_step",
            "p1x_flash_attn_decode_quant"]
 
@@ -98,6 +99,7 @@ def load():
         "p1x_round_to_fp16": (C.c_int, [vp, vp, i64, vp]),
         "p1x_get_rows": (C.c_int, [C.c_int, vp, i64, i64, i64, vp, vp, vp]),
         "p1x_rms_norm_q8_1": (C.c_int, [vp, vp, vp, i64, C.c_float, vp, vp, vp, vp]),
+        "p1x_rms_norm_mul_mat_vec": (C.c_int, [C.c_int, vp, i64, i64, i64, vp, vp, C.c_float, vp, vp]),
         "p1x_swiglu_q8_1": (C.c_int, [vp, vp, i64, vp, vp, vp, vp]),
         "p1x_rope_kv_append": (C.c_int, [vp, vp, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, vp, C.c_float, vp]),
         "p1x_argmax_workspace": (sz, [i64]),
@@ -349,6 +351,21 @@ def rms_norm_q8_1(x, w, eps=1e-5, add=None, want_h=False, stream=None):
     h = torch.empty(n, dtype=torch.float32, device=x.device) if want_h else None
     _check(lib.p1x_rms_norm_q8_1(_ptr(x), _ptr(add), _ptr(w), n, eps, _ptr(qs), _ptr(ds), _ptr(h), _stream(stream)))
     return (Q81(qs, ds), h) if want_h else Q81(qs, ds)
+
+
+def rms_norm_mul_mat_vec(wtype, w, M, K, x, norm_w, eps=1e-5, nb01=None, out=None, stream=None):
+    """y[M] = deq(w) @ Q81(x * rsqrt(mean(x^2) + eps) * norm_w) in one launch (q4_0 / q8_0, K <= 8192): the result
+    of rms_norm_q8_1 (no add) then mul_mat_vec on it, bit for bit."""
+    import torch
+
+    lib = load()
+    wtype = TYPES.get(wtype, wtype)
+    if nb01 is None:
+        nb01 = row_bytes(wtype, K) if wtype in BLOCK else 0
+    y = out if out is not None else torch.empty(M, dtype=torch.float32, device=w.device)
+    _check(lib.p1x_rms_norm_mul_mat_vec(wtype, _ptr(w), nb01, M, K, _ptr(x), _ptr(norm_w), eps, _ptr(y),
+                                        _stream(stream)))
+    return y
 
 
 def swiglu_q8_1(gate, up, want_h=False, stream=None):

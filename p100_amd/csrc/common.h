@@ -157,6 +157,21 @@ __device__ __forceinline__ float quad_xor2(float v) {
     return __builtin_bit_cast(float, quad_xor2_i(__builtin_bit_cast(int, v)));
 }
 
+// Sum over the 64 lanes of a wave, every lane getting it: DPP inside 16-lane rows, then the four row totals. The
+// RMSNorm's sum of squares uses this order wherever it is computed (the standalone norm kernel and the norm
+// prologue of the mat-vec), so both give the same bits.
+__device__ __forceinline__ float norm_wave_total(float v) {
+    v += quad_xor1(v);
+    v += quad_xor2(v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xf, 0xf, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xf, 0xf, true));
+    const int b = __builtin_bit_cast(int, v);
+    return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))) +
+           (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48)));
+}
+
 // Q8_1 of a 32-element block held by a quad of lanes, 8 consecutive elements per lane (lane t of the quad holds
 // elements 8t..8t+7), with the arithmetic of q8_1_store: d = amax/127 and q = round(x/d) (IEEE division), and
 // the sum s in the reference's butterfly order exactly (offsets 16 and 8 are the lane bits 1 and 0 of the quad,

@@ -109,6 +109,23 @@ int p1x_rms_norm_q8_1(float* x, const float* add, const float* w, int64_t n, flo
     return e == hipSuccess ? P1X_OK : hip_fail(e, "rms_norm_q8_1");
 }
 
+int p1x_rms_norm_mul_mat_vec(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K, const float* x,
+                             const float* norm_w, float eps, float* y, void* stream) {
+    if (int rc = ensure_init()) return rc;
+    if (!w || !x || !norm_w || !y) return fail(P1X_EINVAL, "null pointer");
+    if (wtype != P1X_Q4_0 && wtype != P1X_Q8_0) return fail(P1X_EUNSUPPORTED, "weights must be q4_0 or q8_0");
+    if (K <= 0 || K % 32 || K > 8192 || M <= 0 || M > INT32_MAX)
+        return fail(P1X_EINVAL, "K must be a positive multiple of 32, at most 8192, and M positive");
+    if (nb01 < row_bytes(wtype, K) || nb01 % 2) return fail(P1X_EINVAL, "row stride nb01 shorter than a row or odd");
+    if (!(eps >= 0.0f) || !std::isfinite(eps)) return fail(P1X_EINVAL, "eps must be finite and non-negative");
+    if (!aligned(w, 2) || !aligned(x, 16) || !aligned(norm_w, 16) || !aligned(y, 4))
+        return fail(P1X_EINVAL, "x and norm_w must be 16-byte aligned, w 2-byte and y 4-byte");
+    if (!p1x::mmvq_norm_supported(wtype, int(M), int(K))) return fail(P1X_EINVAL, "no kernel for this shape");
+    hipError_t e = p1x::launch_mmvq_norm(wtype, w, nb01, int(M), int(K), p1x::NormArgs{x, norm_w, eps}, y,
+                                         static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? P1X_OK : hip_fail(e, "rms_norm_mul_mat_vec");
+}
+
 int p1x_swiglu_q8_1(const float* gate, const float* up, int64_t n, int8_t* qs, float* ds, float* h_out, void* stream) {
     if (int rc = ensure_init()) return rc;
     if (!gate || !up || !qs || !ds) return fail(P1X_EINVAL, "null pointer");
@@ -231,22 +248,34 @@ int p1x_llama_decode_step(const p1x_llama_model* m, p1x_decode_state* state, con
     const bool down_resid = p1x::mmvq_residual_supported(hp.wtype, E, F);
     const bool swiglu_fused = p1x::mmvq_residual_supported(hp.wtype, 2 * F, E);
     const float* pending = nullptr;
+    // With nothing pending, the attention norm runs inside the q/k/v projection (every work-group normalizes and
+    // quantizes x itself, the same bits as the norm kernel) and takes no launch. The FFN norm keeps its launch: the
+    // gate/up grid is 4.7x larger and repeating the norm in each work-group costs more than the launch.
+    const bool norm_qkv = rope_fused && p1x::mmvq_norm_supported(hp.wtype, E + 2 * kv, E) &&
+                          p1x::mmvq_norm_supported(hp.wtype, E, E) && p1x::mmvq_norm_supported(hp.wtype, kv, E);
     for (int l = 0; l < hp.n_layer; ++l) {
         const p1x_llama_layer& L = m->layers[l];
-        P1X_TRY(p1x::launch_rms_norm_q8_1(x, pending, L.attn_norm, E, hp.rms_eps, qs, ds, nullptr, s),
-                "attention norm");
+        const bool attn_norm_fused = norm_qkv && !pending;
+        if (!attn_norm_fused)
+            P1X_TRY(p1x::launch_rms_norm_q8_1(x, pending, L.attn_norm, E, hp.rms_eps, qs, ds, nullptr, s),
+                    "attention norm");
         const auto* wq = static_cast<const uint8_t*>(L.wq);
         const bool stacked = L.wk == wq + E * nb_w && L.wv == wq + (E + kv) * nb_w;
         if (rope_fused) {  // the projection rotates q / k and appends k / v itself
             p1x::RopeKv rk{qr, L.k_cache, L.v_cache, int(E), int(kv), d, hp.n_ctx, 0, &state->pos, rope_cs};
+            const p1x::NormArgs na{x, L.attn_norm, hp.rms_eps};
+            auto proj = [&](const void* w, int M) {
+                return attn_norm_fused ? p1x::launch_mmvq_norm_rope_kv(hp.wtype, w, nb_w, M, E, na, rk, s)
+                                       : p1x::launch_mmvq_rope_kv(hp.wtype, w, nb_w, M, E, qs, ds, rk, s);
+            };
             if (stacked) {
-                P1X_TRY(p1x::launch_mmvq_rope_kv(hp.wtype, wq, nb_w, E + 2 * kv, E, qs, ds, rk, s), "qkv + rope");
+                P1X_TRY(proj(wq, int(E + 2 * kv)), "qkv + rope");
             } else {
-                P1X_TRY(p1x::launch_mmvq_rope_kv(hp.wtype, L.wq, nb_w, E, E, qs, ds, rk, s), "q + rope");
+                P1X_TRY(proj(L.wq, int(E)), "q + rope");
                 rk.row_base = int(E);
-                P1X_TRY(p1x::launch_mmvq_rope_kv(hp.wtype, L.wk, nb_w, kv, E, qs, ds, rk, s), "k + rope");
+                P1X_TRY(proj(L.wk, int(kv)), "k + rope");
                 rk.row_base = int(E + kv);
-                P1X_TRY(p1x::launch_mmvq_rope_kv(hp.wtype, L.wv, nb_w, kv, E, qs, ds, rk, s), "v");
+                P1X_TRY(proj(L.wv, int(kv)), "v");
             }
         } else {
             if (stacked) {
@@ -277,11 +306,12 @@ int p1x_llama_decode_step(const p1x_llama_model* m, p1x_decode_state* state, con
         }
         P1X_TRY(p1x::launch_rms_norm_q8_1(x, pending, L.ffn_norm, E, hp.rms_eps, qs, ds, nullptr, s), "ffn norm");
         const auto* wg = static_cast<const uint8_t*>(L.w_gate);
-        if (L.w_up == wg + F * nb_w && swiglu_fused) {  // the mat-vec writes silu(gate) * up; then its Q8_1
+        const bool gu_stacked = L.w_up == wg + F * nb_w;
+        if (gu_stacked && swiglu_fused) {  // the mat-vec writes silu(gate) * up; then its Q8_1
             P1X_TRY(p1x::launch_mmvq_swiglu(hp.wtype, wg, nb_w, F, E, qs, ds, gu, s), "gate/up + swiglu");
             P1X_TRY(p1x::launch_quantize_q8_1(gu, qs, ds, F, 1, s), "swiglu quantize");
         } else {
-            if (L.w_up == wg + F * nb_w) {
+            if (gu_stacked) {
                 P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, wg, nb_w, 2 * F, E, qs, ds, nullptr, gu, nullptr, s), "gate/up");
             } else {
                 P1X_TRY(p1x::launch_mmvq(hp.wtype, 1, L.w_gate, nb_w, F, E, qs, ds, nullptr, gu, nullptr, s), "gate");

@@ -437,24 +437,6 @@ __global__ __launch_bounds__(kSplitThreads) void k_fa_split(FaArgs a) {
     }
 }
 
-// Wave max / sum over all 64 lanes (every lane gets the result): DPP inside rows, then swizzle and bpermute.
-__device__ __forceinline__ float wave_max(float v) {
-    v = fmaxf(v, dpp_f<kXor1>(v));
-    v = fmaxf(v, dpp_f<kXor2>(v));
-    v = fmaxf(v, dpp_f<kHalfMirror>(v));
-    v = fmaxf(v, dpp_f<kMirror>(v));
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F)));
-    return fmaxf(v, __shfl_xor(v, 32));
-}
-__device__ __forceinline__ float wave_sum(float v) {
-    v += dpp_f<kXor1>(v);
-    v += dpp_f<kXor2>(v);
-    v += dpp_f<kHalfMirror>(v);
-    v += dpp_f<kMirror>(v);
-    v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
-    return v + __shfl_xor(v, 32);
-}
-
 // The value of lane ^ K (exact permutations): DPP inside 16-lane rows for K < 16 (xor 1 and 2 by quad_perm,
 // xor 4 = row_half_mirror then the quad reversed, xor 8 = row rotation by 8), ds_swizzle for 16, a shuffle for 32.
 template <int K>

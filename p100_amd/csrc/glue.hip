@@ -71,18 +71,6 @@ __device__ __forceinline__ void store_q8_1(const Q81Quad& r, int64_t e0, int8_t*
     *reinterpret_cast<uint2*>(qs + e0) = make_uint2(r.q0, r.q1);
     if ((e0 & 31) == 0) ds[e0 / 32] = make_float4(round_fp16(r.d), round_fp16(r.s), static_cast<float>(r.isum), 0.0f);
 }
-// Sum over the 64 lanes of a wave, every lane getting it: DPP inside 16-lane rows, then the four row totals.
-__device__ __forceinline__ float wave_total(float v) {
-    v += quad_xor1(v);
-    v += quad_xor2(v);
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xf, 0xf, true));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xf, 0xf, true));
-    const int b = __builtin_bit_cast(int, v);
-    return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
-            __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))) +
-           (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
-            __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48)));
-}
 
 // One work-group of blockDim.x = min(1024, n/8 rounded up to a wave) threads: x += add (when add is given; x is the
 // residual stream and is written back), then h = (x * rsqrt(mean(x^2) + eps)) * w (ggml rms_norm then mul, the
@@ -114,7 +102,7 @@ __global__ __launch_bounds__(kNormMaxThreads) void k_rms_norm_q8_1(float* __rest
             for (int e = 0; e < 8; ++e) ss = fmaf(v[r][e], v[r][e], ss);
         }
     }
-    ss = wave_total(ss);
+    ss = norm_wave_total(ss);
     if ((t & 63) == 0) part[t >> 6] = ss;
     __syncthreads();
     float tot = 0.0f;

@@ -28,6 +28,21 @@ struct RopeKv {
 };
 // One column, prepared Q8_1: y = W x added to the residual stream x_res in place (x_res[r] += y[r]), the RMSNorm's
 // residual addition done by the producing mat-vec.
+// The RMSNorm of the residual stream x times w (eps) quantized to Q8_1 inside every work-group of the mat-vec
+// (q4_0 / q8_0, one column, K <= 8192), bit-identical to launch_rms_norm_q8_1 without an add, so the norm takes
+// no launch of its own. Rows stored as they are, or the RoPE + KV-append epilogue. Every work-group repeats the
+// norm (about 40 VALU instructions per element, all on the work-group's critical path), so this pays only where
+// the grid is small: q/k/v (768 work-groups) and o-sized matrices, not the FFN's 28672 rows.
+struct NormArgs {
+    const float* x;
+    const float* w;
+    float eps;
+};
+bool mmvq_norm_supported(int type, int M, int K);
+hipError_t launch_mmvq_norm(int type, const void* w, int64_t nb01, int M, int K, const NormArgs& n, float* y,
+                            hipStream_t stream);
+hipError_t launch_mmvq_norm_rope_kv(int type, const void* w, int64_t nb01, int M, int K, const NormArgs& n,
+                                    const RopeKv& rk, hipStream_t stream);
 bool mmvq_residual_supported(int type, int M, int K);
 hipError_t launch_mmvq_residual(int type, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
                                 float* x_res, hipStream_t stream);

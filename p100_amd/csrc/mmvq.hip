@@ -452,6 +452,94 @@ __global__ __launch_bounds__(256) void k_mmvq_fx(const uint8_t* __restrict__ w, 
 // LDS and no barrier precedes the compute: a work-group reads the activation (48 bytes per 32-block) once, straight
 // from L2 into registers, and the weight stream starts in the same round trip. Units past the row end are clamped
 // to unit 0 and dropped by a select; rows past M are clamped for the loads and never stored.
+// Activation sources of k_mmvr. SrcQ81: a Q8_1 activation prepared in global memory. SrcNorm<NV>: the RMSNorm of
+// the residual stream x times the norm weight w, quantized to Q8_1 by every work-group itself (so the norm needs
+// no launch of its own). Its element ownership and reduction order are those of k_rms_norm_q8_1 at n = K <= 8192
+// (that kernel's 64*ceil(K/512) threads in one pass map to threads t + 256 i, i < NV, here): lane sums of squares
+// over 8 consecutive elements, the same wave sum, the wave totals added in order, rsqrt(mean + eps), (x * scale) *
+// w, Q8_1 by quads. The blocks are therefore bit-identical to that kernel's and go through LDS to their owners.
+struct SrcQ81 {
+    static constexpr int kNV = 0;
+    const int8_t* xq;
+    const float4* xds;
+};
+template <int NV>
+struct SrcNorm {
+    static constexpr int kNV = NV;  // 8-element chunks per thread: K <= 2048 * NV
+    const float* x;
+    const float* w;
+    float eps;
+};
+template <int NV>
+struct NormLds {
+    uint4 lo[64 * NV], hi[64 * NV];  // q[0..15] and q[16..31] of block b
+    float4 ds[64 * NV];
+    float part[4 * NV];  // wave totals of the standalone kernel's waves
+};
+template <>
+struct NormLds<0> {};
+
+template <int NV>
+struct NormIn {
+    float x[NV][8], w[NV][8];
+};
+template <>
+struct NormIn<0> {};
+// Chunk i of thread t: elements 8 (t + 256 i) .. + 7; a chunk past K is read at K - 8 and zeroed (no branch, so
+// the weight loads issued next stay in flight).
+template <int NV>
+__device__ __forceinline__ NormIn<NV> norm_load(const SrcNorm<NV>& src, int K) {
+    NormIn<NV> in;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int e0 = 8 * (int(threadIdx.x) + 256 * i), ec = e0 < K ? e0 : K - 8;
+        const float4* xp = reinterpret_cast<const float4*>(src.x + ec);
+        const float4* wp = reinterpret_cast<const float4*>(src.w + ec);
+        const float4 x0 = xp[0], x1 = xp[1], w0 = wp[0], w1 = wp[1];
+        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        const float ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            in.x[i][e] = e0 < K ? xs[e] : 0.0f;
+            in.w[i][e] = ws[e];
+        }
+    }
+    return in;
+}
+// RMSNorm + Q8_1 of the loaded chunks into LDS (two work-group barriers); every thread of the work-group calls it.
+template <int NV>
+__device__ __forceinline__ void norm_q8_1_to_lds(const NormIn<NV>& in, int K, float eps, NormLds<NV>& l) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nwv = (K / 8 + 63) / 64;  // waves of the standalone kernel (one pass)
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(in.x[i][e], in.x[i][e], ss);
+        ss = norm_wave_total(ss);
+        if (lane == 0 && wave + 4 * i < nwv) l.part[wave + 4 * i] = ss;
+    }
+    __syncthreads();
+    float tot = 0.0f;
+    for (int k = 0; k < nwv; ++k) tot += l.part[k];
+    const float scale = rsqrtf(tot / float(K) + eps);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int vl = tid + 256 * i;
+        float hv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) hv[e] = (in.x[i][e] * scale) * in.w[i][e];
+        const Q81Quad r = q8_1_quad(hv);
+        if (8 * vl < K) {
+            const int b = vl >> 2, qd = vl & 3;
+            uint2* dst = reinterpret_cast<uint2*>(qd < 2 ? &l.lo[b] : &l.hi[b]) + (qd & 1);
+            *dst = make_uint2(r.q0, r.q1);
+            if (qd == 0) l.ds[b] = make_float4(round_fp16(r.d), round_fp16(r.s), static_cast<float>(r.isum), 0.0f);
+        }
+    }
+    __syncthreads();
+}
+
 // Epilogues of k_mmvr: the row sums stored as they are, or one token's q/k/v rows rotated in adjacent pairs and
 // appended to the KV cache (RopeKv; R is even there, so a row-group holds whole pairs).
 // An epilogue's `start` runs before the weight stream is requested (its own loads go first) and `prepare` once the
@@ -550,10 +638,9 @@ struct EpiSwiGLU {
     }
 };
 
-template <int TYPE, int NWK, int UPT, int R, bool SUMS, class EPI>
+template <int TYPE, int NWK, int UPT, int R, bool SUMS, class EPI, class SRC>
 __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int64_t nb01, int M, int K,
-                                              const int8_t* __restrict__ xq, const float4* __restrict__ xds,
-                                              const EPI epi, int32_t* __restrict__ gs) {
+                                              const SRC src, const EPI epi, int32_t* __restrict__ gs) {
     static_assert(!EPI::kPairs || R % 2 == 0, "row pairs stay inside one row-group");
 
     using U = typename UnitOf<TYPE>::T;
@@ -564,16 +651,18 @@ __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int
     const int units = K / U::kElems;
     const int row0 = (blockIdx.x * G + g) * R;
     const int epi_in = epi.start();
-    const ActGlobal act{xq, xds, K};
+    constexpr int NV = SRC::kNV;
     ActBlock x[UPT];
     int uc[UPT];
     bool uok[UPT];
+    NormIn<NV> nin;
+    if constexpr (NV > 0) nin = norm_load(src, K);  // requested ahead of the weights: waited for first
 #pragma unroll
     for (int j = 0; j < UPT; ++j) {
         const int u = t + T * j;
         uok[j] = u < units;
         uc[j] = uok[j] ? u : 0;
-        x[j] = act.get(0, uc[j]);
+        if constexpr (NV == 0) x[j] = ActGlobal{src.xq, src.xds, K}.get(0, uc[j]);
     }
     U wv[R][UPT];
 #pragma unroll
@@ -583,6 +672,13 @@ __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int
         for (int j = 0; j < UPT; ++j) wv[r][j].load(wr, uc[j]);
     }
     const auto est = epi.template prepare<R>(epi_in, row0, M);
+    if constexpr (NV > 0) {  // the weight stream stays in flight across the barriers (they wait for LDS only)
+        __shared__ NormLds<NV> nl;
+        norm_q8_1_to_lds(nin, K, src.eps, nl);
+        const ActLds al{nl.lo, nl.hi, nl.ds, units};
+#pragma unroll
+        for (int j = 0; j < UPT; ++j) x[j] = al.get(0, uc[j]);
+    }
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -654,29 +750,42 @@ bool mmvr_plan(int type, int M, int K, MmvrPlan& p) {
     return true;
 }
 
-template <int TYPE, class EPI>
-hipError_t launch_mmvr(const MmvrPlan& p, const uint8_t* w, int64_t nb01, int M, int K, const int8_t* xq,
-                       const float4* xds, const EPI& epi, int32_t* gs, hipStream_t stream) {
+template <int TYPE, class EPI, class SRC>
+hipError_t launch_mmvr(const MmvrPlan& p, const uint8_t* w, int64_t nb01, int M, int K, const SRC& src,
+                       const EPI& epi, int32_t* gs, hipStream_t stream) {
 #define P1X_MMVR(NW, UP, RR)                                                                                        \
     if (p.nwk == NW && p.upt == UP && p.r == RR) {                                                                 \
         const dim3 grid((M + (4 / NW) * RR - 1) / ((4 / NW) * RR));                                                \
-        if (gs)                                                                                                    \
-            hipLaunchKernelGGL((k_mmvr<TYPE, NW, UP, RR, true, EPI>), grid, dim3(256), 0, stream, w, nb01, M, K, xq, xds, \
-                               epi, gs);                                                                           \
-        else                                                                                                       \
-            hipLaunchKernelGGL((k_mmvr<TYPE, NW, UP, RR, false, EPI>), grid, dim3(256), 0, stream, w, nb01, M, K, xq,   \
-                               xds, epi, gs);                                                                      \
+        if constexpr (SRC::kNV == 0) {                                                                             \
+            if (gs) {                                                                                              \
+                hipLaunchKernelGGL((k_mmvr<TYPE, NW, UP, RR, true, EPI, SRC>), grid, dim3(256), 0, stream, w, nb01, M, \
+                                   K, src, epi, gs);                                                               \
+                return hipGetLastError();                                                                          \
+            }                                                                                                      \
+        }                                                                                                          \
+            hipLaunchKernelGGL((k_mmvr<TYPE, NW, UP, RR, false, EPI, SRC>), grid, dim3(256), 0, stream, w, nb01, M, K,  \
+                               src, epi, gs);                                                                      \
         return hipGetLastError();                                                                                  \
     }
-    P1X_MMVR(1, 1, 2)
-    if constexpr (!EPI::kPairs) {
-        P1X_MMVR(1, 2, 1)
+    if constexpr (SRC::kNV == 1) {  // the norm prologue: mmvr_norm_plan's shapes for each row length
+        P1X_MMVR(1, 1, 2)
+    } else if constexpr (SRC::kNV == 2) {
+        P1X_MMVR(1, 2, 2)
+        P1X_MMVR(2, 1, 2)
+        P1X_MMVR(2, 1, 4)
+    } else if constexpr (SRC::kNV == 4) {
+        P1X_MMVR(2, 2, 2)
+    } else {
+        P1X_MMVR(1, 1, 2)
+        if constexpr (!EPI::kPairs) {
+            P1X_MMVR(1, 2, 1)
+        }
+        P1X_MMVR(1, 2, 2)
+        P1X_MMVR(2, 1, 2)
+        P1X_MMVR(2, 1, 4)
+        P1X_MMVR(2, 2, 2)
+        P1X_MMVR(4, 2, 4)
     }
-    P1X_MMVR(1, 2, 2)
-    P1X_MMVR(2, 1, 2)
-    P1X_MMVR(2, 1, 4)
-    P1X_MMVR(2, 2, 2)
-    P1X_MMVR(4, 2, 4)
 #undef P1X_MMVR
     return hipErrorInvalidValue;
 }
@@ -879,8 +988,8 @@ hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int 
         return type == Q4_0 ? launch_mmvr_cols<Q4_0>(plan, B, wb, nb01, M, K, xq, d4, y, gs, stream)
                             : launch_mmvr_cols<Q8_0>(plan, B, wb, nb01, M, K, xq, d4, y, gs, stream);
     if (B == 1 && !x && P1X_MMVR_ENABLE && (type == Q4_0 || type == Q8_0) && mmvr_plan(type, M, K, plan))
-        return type == Q4_0 ? launch_mmvr<Q4_0>(plan, wb, nb01, M, K, xq, d4, EpiRows{y, nullptr}, gs, stream)
-                            : launch_mmvr<Q8_0>(plan, wb, nb01, M, K, xq, d4, EpiRows{y, nullptr}, gs, stream);
+        return type == Q4_0 ? launch_mmvr<Q4_0>(plan, wb, nb01, M, K, SrcQ81{xq, d4}, EpiRows{y, nullptr}, gs, stream)
+                            : launch_mmvr<Q8_0>(plan, wb, nb01, M, K, SrcQ81{xq, d4}, EpiRows{y, nullptr}, gs, stream);
     switch (type) {
         case Q4_0: return launch_type<Q4_0>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
         case Q8_0: return launch_type<Q8_0>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
@@ -888,6 +997,46 @@ hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int 
         case Q6_K: return launch_type<Q6_K>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
     }
     return hipErrorInvalidValue;
+}
+
+// Plan of the norm-prologue form: mmvr_plan's row-group shape with at least 2 rows (the per-row arithmetic does not
+// depend on R, so the rows equal the prepared-activation kernel's bit for bit), K <= 8192.
+bool mmvr_norm_plan(int type, int M, int K, MmvrPlan& p) {
+    if (!P1X_MMVR_ENABLE || (type != Q4_0 && type != Q8_0) || K > 8192 || !mmvr_plan(type, M, K, p)) return false;
+    if (p.r == 1) p.r = 2;
+    return true;
+}
+
+template <int TYPE, class EPI>
+hipError_t launch_mmvr_norm(const MmvrPlan& p, const uint8_t* w, int64_t nb01, int M, int K, const NormArgs& n,
+                            const EPI& epi, hipStream_t stream) {
+    const int units = K / 32;
+    if (units <= 64) return launch_mmvr<TYPE>(p, w, nb01, M, K, SrcNorm<1>{n.x, n.w, n.eps}, epi, nullptr, stream);
+    if (units <= 128) return launch_mmvr<TYPE>(p, w, nb01, M, K, SrcNorm<2>{n.x, n.w, n.eps}, epi, nullptr, stream);
+    return launch_mmvr<TYPE>(p, w, nb01, M, K, SrcNorm<4>{n.x, n.w, n.eps}, epi, nullptr, stream);
+}
+
+bool mmvq_norm_supported(int type, int M, int K) {
+    MmvrPlan plan;
+    return mmvr_norm_plan(type, M, K, plan);
+}
+
+hipError_t launch_mmvq_norm(int type, const void* w, int64_t nb01, int M, int K, const NormArgs& n, float* y,
+                            hipStream_t stream) {
+    MmvrPlan plan;
+    if (!mmvr_norm_plan(type, M, K, plan)) return hipErrorInvalidValue;
+    const auto* wb = static_cast<const uint8_t*>(w);
+    return type == Q4_0 ? launch_mmvr_norm<Q4_0>(plan, wb, nb01, M, K, n, EpiRows{y, nullptr}, stream)
+                        : launch_mmvr_norm<Q8_0>(plan, wb, nb01, M, K, n, EpiRows{y, nullptr}, stream);
+}
+
+hipError_t launch_mmvq_norm_rope_kv(int type, const void* w, int64_t nb01, int M, int K, const NormArgs& n,
+                                    const RopeKv& rk, hipStream_t stream) {
+    MmvrPlan plan;
+    if (M % 2 || rk.d % 2 || !mmvr_norm_plan(type, M, K, plan)) return hipErrorInvalidValue;
+    const auto* wb = static_cast<const uint8_t*>(w);
+    return type == Q4_0 ? launch_mmvr_norm<Q4_0>(plan, wb, nb01, M, K, n, EpiRopeKv{rk}, stream)
+                        : launch_mmvr_norm<Q8_0>(plan, wb, nb01, M, K, n, EpiRopeKv{rk}, stream);
 }
 
 bool mmvq_residual_supported(int type, int M, int K) {
@@ -901,8 +1050,8 @@ hipError_t launch_mmvq_residual(int type, const void* w, int64_t nb01, int M, in
     if (!mmvq_residual_supported(type, M, K) || !mmvr_plan(type, M, K, plan)) return hipErrorInvalidValue;
     const auto* wb = static_cast<const uint8_t*>(w);
     const auto* d4 = reinterpret_cast<const float4*>(xds);
-    return type == Q4_0 ? launch_mmvr<Q4_0>(plan, wb, nb01, M, K, xq, d4, EpiRows{x, x}, nullptr, stream)
-                        : launch_mmvr<Q8_0>(plan, wb, nb01, M, K, xq, d4, EpiRows{x, x}, nullptr, stream);
+    return type == Q4_0 ? launch_mmvr<Q4_0>(plan, wb, nb01, M, K, SrcQ81{xq, d4}, EpiRows{x, x}, nullptr, stream)
+                        : launch_mmvr<Q8_0>(plan, wb, nb01, M, K, SrcQ81{xq, d4}, EpiRows{x, x}, nullptr, stream);
 }
 
 hipError_t launch_mmvq_swiglu(int type, const void* w, int64_t nb01, int F, int K, const int8_t* xq, const float* xds,
@@ -912,8 +1061,8 @@ hipError_t launch_mmvq_swiglu(int type, const void* w, int64_t nb01, int F, int 
     if (plan.r == 1) plan.r = 2;  // the same per-row arithmetic, whole (gate, up) pairs per row-group
     const auto* wb = static_cast<const uint8_t*>(w);
     const auto* d4 = reinterpret_cast<const float4*>(xds);
-    return type == Q4_0 ? launch_mmvr<Q4_0>(plan, wb, nb01, 2 * F, K, xq, d4, EpiSwiGLU{h, F}, nullptr, stream)
-                        : launch_mmvr<Q8_0>(plan, wb, nb01, 2 * F, K, xq, d4, EpiSwiGLU{h, F}, nullptr, stream);
+    return type == Q4_0 ? launch_mmvr<Q4_0>(plan, wb, nb01, 2 * F, K, SrcQ81{xq, d4}, EpiSwiGLU{h, F}, nullptr, stream)
+                        : launch_mmvr<Q8_0>(plan, wb, nb01, 2 * F, K, SrcQ81{xq, d4}, EpiSwiGLU{h, F}, nullptr, stream);
 }
 
 bool mmvq_rope_kv_supported(int type, int M, int K, int d) {
@@ -928,8 +1077,8 @@ hipError_t launch_mmvq_rope_kv(int type, const void* w, int64_t nb01, int M, int
     if (plan.r == 1) plan.r = 2;  // the same per-row arithmetic (rows never share sums), whole pairs per row-group
     const auto* wb = static_cast<const uint8_t*>(w);
     const auto* d4 = reinterpret_cast<const float4*>(xds);
-    return type == Q4_0 ? launch_mmvr<Q4_0>(plan, wb, nb01, M, K, xq, d4, EpiRopeKv{rk}, nullptr, stream)
-                        : launch_mmvr<Q8_0>(plan, wb, nb01, M, K, xq, d4, EpiRopeKv{rk}, nullptr, stream);
+    return type == Q4_0 ? launch_mmvr<Q4_0>(plan, wb, nb01, M, K, SrcQ81{xq, d4}, EpiRopeKv{rk}, nullptr, stream)
+                        : launch_mmvr<Q8_0>(plan, wb, nb01, M, K, SrcQ81{xq, d4}, EpiRopeKv{rk}, nullptr, stream);
 }
 
 }  // namespace p1x

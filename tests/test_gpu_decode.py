@@ -103,6 +103,35 @@ def test_rms_norm_q8_1(orc, gpu, n):
     assert np.max(np.abs(h2.cpu().numpy() - r2)) <= 2e-6 * np.max(np.abs(r2))
 
 
+@pytest.mark.parametrize("tname", ["q4_0", "q8_0"])
+def test_rms_norm_mul_mat_vec_matches_two_ops(orc, gpu, tname):
+    """The norm computed inside the mat-vec equals p1x_rms_norm_q8_1 (no add) + p1x_mul_mat_vec_q8_1, bit for bit,
+    for every row-group shape the fused form uses (K 1024 .. 8192, M from a few rows to the FFN's stacked gate/up);
+    x keeps an all-zero block and a large outlier."""
+    t = orc.TYPES[tname]
+    cases = [(9, 1024), (1024, 4096), (4100, 4096), (6144, 4096), (28672, 4096), (1000, 4064), (300, 8192),
+             (77, 2048), (5, 32)]
+    for M, K in cases:
+        rng = np.random.default_rng(M * 7 + K)
+        x = (rng.standard_normal(K) * 2.5).astype(np.float32)
+        x[:32] = 0.0
+        if K > 64:
+            x[40] = np.float32(300.0)
+        nw = (1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+        r = orc.Rng(M + K)
+        w = np.stack([r.random_row(t, K) for _ in range(min(M, 64))])
+        w = np.tile(w, (M // len(w) + 1, 1))[:M]  # repeated rows keep the host side quick at large M
+        wd, xd, nwd = to_dev(w), to_dev(x), to_dev(nw)
+        y = P.rms_norm_mul_mat_vec(t, wd, M, K, xd, nwd, eps=1e-5).cpu().numpy()
+        q = P.rms_norm_q8_1(to_dev(x), nwd, eps=1e-5)
+        y2 = P.mul_mat_vec(t, wd, M, K, q).cpu().numpy()[0]
+        assert np.array_equal(y.view(np.uint32), y2.view(np.uint32)), (M, K)
+        assert np.array_equal(xd.cpu().numpy(), x)  # x is only read
+    with pytest.raises(ValueError):  # K above 8192
+        P.rms_norm_mul_mat_vec(t, to_dev(np.zeros((4, 9216 // 32 * (18 if tname == "q4_0" else 34)), np.uint8)),
+                               4, 9216, to_dev(np.zeros(9216, np.float32)), to_dev(np.ones(9216, np.float32)))
+
+
 # ------------------------------------------------------------------------------------------------ swiglu
 @pytest.mark.parametrize("n", [32, 14336])
 def test_swiglu_q8_1(orc, gpu, n):
