@@ -97,7 +97,10 @@ __global__ __launch_bounds__(64 * kMmqWaves) void k_mmq_mfma(const uint8_t* __re
 
     // Global side of the staging: lane (row lane/4, quarter lane%4) reads NWL x 16 bytes of its row's dword-aligned
     // span.
-    const auto wr = rsrc(w, uint32_t(size_t(M) * nb01));
+    // The range check zeroes every dword not wholly inside the resource, so its size is rounded up to a whole
+    // dword: with q8_0 rows of an odd block count M * nb01 ends mid-dword, and the last row's last quants would
+    // read as zeros. The bytes past the end share that dword (and its page) with the matrix.
+    const auto wr = rsrc(w, uint32_t((size_t(M) * nb01 + 3) & ~size_t(3)));
     const int srow = lane >> 2, sq = lane & 3;
     const uint32_t srow_off = uint32_t(size_t(min(m0 + srow, M - 1)) * nb01);
     const auto xr = rsrc(xq, uint32_t(size_t(B) * K));          // columns past B read zeros
@@ -222,10 +225,15 @@ __global__ __launch_bounds__(64 * kMmqWaves) void k_mmq_mfma(const uint8_t* __re
 bool mmq_supported(int type, int B) { return (type == Q4_0 || type == Q8_0) && B >= 1 && B <= kMmqMaxCols; }
 // The staging loads address the weight matrix through one 32-bit buffer range.
 bool mmq_fits(int M, int64_t nb01, int K, int B) {
-    return int64_t(M) * nb01 <= int64_t(kOob) && int64_t(B) * K <= int64_t(kOob) &&
+    return int64_t(M) * nb01 + 3 <= int64_t(kOob) && int64_t(B) * K <= int64_t(kOob) &&
            int64_t(B) * (K / 32) * 16 <= int64_t(kOob);
 }
-bool mmq_preferred(int type, int B) { return mmq_supported(type, B) && B >= P1X_MMQ_MIN_COLS; }
+// From 9 columns always; also q8_0 rows longer than 8192 at 7-8 columns, where the dot4 kernel's LDS-staged
+// activation (7-8 x 14336 x 1.5 bytes per work-group) outweighs the matrix-core form (q8_0 4096x14336, graph period:
+// 8 columns 43.2 -> 35.7 us, 7 columns 36.1 -> 35.8; q4_0 and K <= 8192 stay faster on dot4 at <= 8 columns).
+bool mmq_preferred(int type, int B, int K) {
+    return mmq_supported(type, B) && (B >= P1X_MMQ_MIN_COLS || (type == Q8_0 && B >= 7 && K > 8192));
+}
 
 hipError_t launch_mmq(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
                       float* y, int32_t* gs, hipStream_t stream) {

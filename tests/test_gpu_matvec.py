@@ -160,13 +160,31 @@ def test_mmvq_parity(orc, gpu, tname):
 @pytest.mark.parametrize("tname", ["q4_0", "q8_0"])
 def test_many_columns_parity(orc, gpu, tname):
     """9..16 activation columns (the int8 matrix-core form): int32 group sums bit-exact, FP32 within the bars;
-    K of one and two blocks (idle waves in the K split), partial 16-row tiles, and a full-size shape."""
+    K of one and two blocks (idle waves in the K split), partial 16-row tiles, a full-size shape, and q8_0 matrices
+    whose byte size ends mid-dword (odd block counts: the last row's last block is read through the rounded range)."""
     import p100_amd as P
 
     t = orc.TYPES[tname]
-    for k, rows in ((32, 17), (64, 33), (96, 16), (4096, 17), (14336, 33), (4096, 4096)):
+    for k, rows in ((32, 17), (64, 33), (96, 16), (96, 17), (4128, 17), (4096, 17), (14336, 33), (4096, 4096)):
         for ncols in ((9, 12, 16) if rows < 4096 else (16,)):
             w, x = make_case(orc, t, k, rows, ncols, seed=900 + k + rows + ncols)
+            y, sums = P.mul_mat_vec(t, to_dev(w), rows, k, to_dev(x), act="q8_1", group_sums=True)
+            check_matvec(orc, t, w, x, y.cpu().numpy(), sums.cpu().numpy(), "q81")
+            y2 = P.mul_mat_vec(t, to_dev(w), rows, k, to_dev(x), act="q8_1").cpu().numpy()
+            y3 = P.mul_mat_vec(t, to_dev(w), rows, k, P.quantize_q8_1(to_dev(x))).cpu().numpy()
+            assert (y2.view(np.uint32) == y.cpu().numpy().view(np.uint32)).all()
+            assert (y3.view(np.uint32) == y2.view(np.uint32)).all()
+
+
+def test_q8_0_long_rows_seven_eight_columns(orc, gpu):
+    """q8_0 rows longer than 8192 at 7 and 8 columns take the matrix-core form: sums bit-exact, FP32 within the
+    bars, the same bits through the fp32 op and a prepared activation."""
+    import p100_amd as P
+
+    t = orc.TYPES["q8_0"]
+    for k, rows in ((8224, 19), (14336, 40)):
+        for ncols in (7, 8):
+            w, x = make_case(orc, t, k, rows, ncols, seed=700 + k + rows + ncols)
             y, sums = P.mul_mat_vec(t, to_dev(w), rows, k, to_dev(x), act="q8_1", group_sums=True)
             check_matvec(orc, t, w, x, y.cpu().numpy(), sums.cpu().numpy(), "q81")
             y2 = P.mul_mat_vec(t, to_dev(w), rows, k, to_dev(x), act="q8_1").cpu().numpy()
