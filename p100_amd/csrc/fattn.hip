@@ -54,7 +54,9 @@ constexpr int kDimsPerLane = P1X_FA_DPL;
 #endif
 constexpr int kWaves = P1X_FA_WAVES;
 constexpr int kSplitThreads = 64 * kWaves;
-constexpr int kCombineWaves = 4;  // pass-2 work-group: one output row per wave
+// Pass-2 work-group: one wave, one output row (a work-group per row spreads the rows' loads over more CUs; 4 rows per
+// work-group measured 14.1 against 13.4 us at ctx 8192).
+constexpr int kCombineWaves = 1;
 constexpr int kMaxSplits = 256;  // fa_split_plan never exceeds this
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -528,15 +530,15 @@ __device__ __forceinline__ void q8_1_row(const float* v, size_t col0, int8_t* __
     if (col0 % 32 == 0) ds[col0 / 32] = make_float4(round_fp16(d), round_fp16(t[0]), static_cast<float>(isum), 0.0f);
 }
 
-// Pass 2: one wave per output row (four rows per work-group). Lane l owns columns [CPL l, CPL l + CPL) of every
+// Pass 2: one wave (and work-group) per output row. Lane l owns columns [CPL l, CPL l + CPL) of every
 // split's partial, so the weighted sum over splits needs no cross-lane reduction; the split maxima and sums
 // are reduced across lanes once. All loads of a round (kRound splits) are issued before any arithmetic.
 // The combine of fattn-common.cuh:963-977 as modelled in attention_tiled_model.cpp:183-222: rebase each split
 // to the common max, sum, divide once.
-template <int D, int NH>
-__global__ __launch_bounds__(256) void k_fa_combine(FaArgs a, int rows) {
+template <int D, int NH, int RND>
+__global__ __launch_bounds__(64 * kCombineWaves) void k_fa_combine(FaArgs a, int rows) {
     constexpr int CPL = D / 64;  // columns per lane
-    constexpr int kRound = 32;   // splits per round of loads
+    constexpr int kRound = RND;  // splits per round of loads (divides 64)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row = blockIdx.x * kCombineWaves + wave;
     if (row >= rows) return;  // whole wave; nothing below synchronizes across waves
@@ -623,8 +625,15 @@ hipError_t launch_split(const FaArgs& a, int batch, hipStream_t stream) {
     }
     if (a.splits == 1) return hipGetLastError();  // the split pass wrote O and LSE
     const int rows = batch * a.hq * a.seq_q;
-    hipLaunchKernelGGL((k_fa_combine<D, NH>), dim3((rows + kCombineWaves - 1) / kCombineWaves), dim3(64 * kCombineWaves),
-                       0, stream, a, rows);
+    // Splits per round of partial loads: the smallest of 8, 16, 32 covering the plan (loads past the last split
+    // repeat a valid row with weight 0, so a round sized to the plan issues no wasted requests).
+    const dim3 cgrid((rows + kCombineWaves - 1) / kCombineWaves), cblock(64 * kCombineWaves);
+    if (a.splits <= 8)
+        hipLaunchKernelGGL((k_fa_combine<D, NH, 8>), cgrid, cblock, 0, stream, a, rows);
+    else if (a.splits <= 16)
+        hipLaunchKernelGGL((k_fa_combine<D, NH, 16>), cgrid, cblock, 0, stream, a, rows);
+    else
+        hipLaunchKernelGGL((k_fa_combine<D, NH, 32>), cgrid, cblock, 0, stream, a, rows);
     return hipGetLastError();
 }
 
