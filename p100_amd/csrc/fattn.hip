@@ -54,9 +54,6 @@ constexpr int kDimsPerLane = P1X_FA_DPL;
 #endif
 constexpr int kWaves = P1X_FA_WAVES;
 constexpr int kSplitThreads = 64 * kWaves;
-// Pass-2 work-group: one wave, one output row (a work-group per row spreads the rows' loads over more CUs; 4 rows per
-// work-group measured 14.1 against 13.4 us at ctx 8192).
-constexpr int kCombineWaves = 1;
 constexpr int kMaxSplits = 256;  // fa_split_plan never exceeds this
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -535,18 +532,17 @@ __device__ __forceinline__ void q8_1_row(const float* v, size_t col0, int8_t* __
 // are reduced across lanes once. All loads of a round (kRound splits) are issued before any arithmetic.
 // The combine of fattn-common.cuh:963-977 as modelled in attention_tiled_model.cpp:183-222: rebase each split
 // to the common max, sum, divide once.
-template <int D, int NH, int RND>
-__global__ __launch_bounds__(64 * kCombineWaves) void k_fa_combine(FaArgs a, int rows) {
+template <int D, int NH, int RND, int NML>
+__global__ __launch_bounds__(64) void k_fa_combine(FaArgs a) {
     constexpr int CPL = D / 64;  // columns per lane
     constexpr int kRound = RND;  // splits per round of loads (divides 64)
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row = blockIdx.x * kCombineWaves + wave;
-    if (row >= rows) return;  // whole wave; nothing below synchronizes across waves
-    // Output row (b, h, i) -> group of the split pass and head slot hh inside it.
-    const int i = row % a.seq_q, bh = row / a.seq_q, h = bh % a.hq, b = bh / a.hq;
-    const int group = a.hq / a.hkv, kvh = h / group, rem = h % group, hc = rem / NH, hh = rem % NH;
-    const int grp = ((b * a.hkv + kvh) * a.head_chunks + hc) * a.seq_q + i;
-    const size_t base = size_t(grp) * a.splits * NH + hh;  // partial of split s: base + s * NH
+    const int lane = threadIdx.x;
+    // Grid (query row i, head rem inside its GQA group, batch * KV head): the output row and the split pass's group
+    // and head slot follow without a division. Output row (b, h = kvh * group + rem, i).
+    const int i = blockIdx.x, rem = blockIdx.y, bkv = blockIdx.z, group = a.head_chunks * NH;
+    const int row = (bkv * group + rem) * a.seq_q + i;
+    const int grp = (bkv * a.head_chunks + rem / NH) * a.seq_q + i;
+    const size_t base = size_t(grp) * a.splits * NH + rem % NH;  // partial of split s: base + s * NH
 
     const float* po = a.part_o + base * D + CPL * lane;
     float buf[kRound][CPL];
@@ -567,19 +563,19 @@ __global__ __launch_bounds__(64 * kCombineWaves) void k_fa_combine(FaArgs a, int
         }
     };
     load_round(0);  // the first round of partial rows is in flight together with the split statistics
-    float2 ml[kMaxSplits / 64];
+    float2 ml[NML];  // statistics of split lane + 64 k (NML * 64 >= splits)
 #pragma unroll
-    for (int k = 0; k < kMaxSplits / 64; ++k) {
+    for (int k = 0; k < NML; ++k) {
         const int sp = lane + 64 * k;
         ml[k] = sp < a.splits ? a.part_ml[base + size_t(sp) * NH] : make_float2(-INFINITY, 0.0f);
     }
     float mx = ml[0].x;
 #pragma unroll
-    for (int k = 1; k < kMaxSplits / 64; ++k) mx = fmaxf(mx, ml[k].x);
+    for (int k = 1; k < NML; ++k) mx = fmaxf(mx, ml[k].x);
     mx = wave_max_rl(mx);
-    float den = 0.0f, wv[kMaxSplits / 64];  // weight of split lane + 64 k, held by that lane
+    float den = 0.0f, wv[NML];  // weight of split lane + 64 k, held by that lane (0 past the last split)
 #pragma unroll
-    for (int k = 0; k < kMaxSplits / 64; ++k) {
+    for (int k = 0; k < NML; ++k) {
         wv[k] = (ml[k].y == 0.0f || mx == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ml[k].x - mx);
         den = fmaf(wv[k], ml[k].y, den);
     }
@@ -592,12 +588,11 @@ __global__ __launch_bounds__(64 * kCombineWaves) void k_fa_combine(FaArgs a, int
         if (s0 > 0) load_round(s0);
         float wk = wv[0];  // the register holding splits s0 .. s0 + kRound - 1 (a wave-uniform choice)
 #pragma unroll
-        for (int k = 1; k < kMaxSplits / 64; ++k) wk = (s0 >> 6) == k ? wv[k] : wk;
+        for (int k = 1; k < NML; ++k) wk = (s0 >> 6) == k ? wv[k] : wk;
 #pragma unroll
-        for (int u = 0; u < kRound; ++u) {
-            const float ww = s0 + u < a.splits ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                     __builtin_bit_cast(int, wk), (s0 & 63) + u))
-                                               : 0.0f;
+        for (int u = 0; u < kRound; ++u) {  // a split past the last has weight 0 (and a valid row in buf)
+            const float ww = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk),
+                                                                                 (s0 & 63) + u));
 #pragma unroll
             for (int c = 0; c < CPL; ++c) acc[c] = fmaf(ww, buf[u][c], acc[c]);
         }
@@ -624,16 +619,18 @@ hipError_t launch_split(const FaArgs& a, int batch, hipStream_t stream) {
         default: hipLaunchKernelGGL((k_fa_split<D, NH, 3, KT>), grid, dim3(kSplitThreads), 0, stream, a); break;
     }
     if (a.splits == 1) return hipGetLastError();  // the split pass wrote O and LSE
-    const int rows = batch * a.hq * a.seq_q;
     // Splits per round of partial loads: the smallest of 8, 16, 32 covering the plan (loads past the last split
-    // repeat a valid row with weight 0, so a round sized to the plan issues no wasted requests).
-    const dim3 cgrid((rows + kCombineWaves - 1) / kCombineWaves), cblock(64 * kCombineWaves);
+    // repeat a valid row with weight 0, so a round sized to the plan issues no wasted requests); split statistics
+    // in one register up to 64 splits.
+    const dim3 cgrid(a.seq_q, a.head_chunks * NH, batch * a.hkv);
     if (a.splits <= 8)
-        hipLaunchKernelGGL((k_fa_combine<D, NH, 8>), cgrid, cblock, 0, stream, a, rows);
+        hipLaunchKernelGGL((k_fa_combine<D, NH, 8, 1>), cgrid, dim3(64), 0, stream, a);
     else if (a.splits <= 16)
-        hipLaunchKernelGGL((k_fa_combine<D, NH, 16>), cgrid, cblock, 0, stream, a, rows);
+        hipLaunchKernelGGL((k_fa_combine<D, NH, 16, 1>), cgrid, dim3(64), 0, stream, a);
+    else if (a.splits <= 64)
+        hipLaunchKernelGGL((k_fa_combine<D, NH, 32, 1>), cgrid, dim3(64), 0, stream, a);
     else
-        hipLaunchKernelGGL((k_fa_combine<D, NH, 32>), cgrid, cblock, 0, stream, a, rows);
+        hipLaunchKernelGGL((k_fa_combine<D, NH, 32, kMaxSplits / 64>), cgrid, dim3(64), 0, stream, a);
     return hipGetLastError();
 }
 
