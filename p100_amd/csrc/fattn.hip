@@ -61,6 +61,17 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 #ifndef P1X_FA_AUX
 #define P1X_FA_AUX 2  // buffer-load cache policy: non-temporal (each K/V element is read once)
 #endif
+// ceil(n / d) for wave-uniform 0 <= n < 2^24, 0 < d: a reciprocal estimate (within one of the quotient, exact
+// integers in fp32) and two exact corrections instead of the integer division sequence; larger n divide.
+__device__ __forceinline__ int ceil_div_uniform(int n, int d) {
+    const int num = n + d - 1;
+    if (num >= (1 << 24)) return num / d;
+    int q = int(float(num) * __builtin_amdgcn_rcpf(float(d)));
+    q += (q + 1) * d <= num ? 1 : 0;
+    q -= q * d > num ? 1 : 0;
+    return q;
+}
+
 // K/V rows of one (batch, KV head) through a buffer resource: the hardware range check turns any offset at or
 // past `bytes` into a load of zeros that touches no memory, so loads can be issued unconditionally.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t kv_rsrc(const __half* base, uint32_t bytes) {
@@ -185,10 +196,17 @@ __global__ __launch_bounds__(kSplitThreads) void k_fa_split(FaArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane / LPK, l = lane % LPK;
     const int split = blockIdx.x;
-    const int kvh_all = blockIdx.y / a.head_chunks, hc = blockIdx.y % a.head_chunks;
-    const int b = kvh_all / a.hkv, kvh = kvh_all % a.hkv;
+    // blockIdx.y = (b * hkv + kvh) * head_chunks + hc. The divisions take uniform branches for the common cases
+    // (1, 2 or 4 head chunks; one sequence), ahead of every address the kernel forms.
+    int kvh_all, b, kvh;
+    if (a.head_chunks == 2) kvh_all = int(blockIdx.y) >> 1;
+    else if (a.head_chunks == 1) kvh_all = blockIdx.y;
+    else kvh_all = int(blockIdx.y) / a.head_chunks;
+    const int hc = blockIdx.y - kvh_all * a.head_chunks;
+    if (kvh_all < a.hkv) b = 0, kvh = kvh_all;
+    else b = kvh_all / a.hkv, kvh = kvh_all - b * a.hkv;
     const int i = blockIdx.z;
-    const int h0 = kvh * (a.hq / a.hkv) + hc * NH;
+    const int h0 = (kvh * a.head_chunks + hc) * NH;  // the GQA group is head_chunks * NH query heads
     // Chunk c of this lane holds dimensions [c*D/CH + 8l, c*D/CH + 8l + 8): each load instruction of a wave
     // covers the same 1/CH slice of GPW consecutive rows (whole 128-byte lines).
     auto dim0 = [&](int c) { return c * (D / CH) + 8 * l; };
@@ -199,7 +217,8 @@ __global__ __launch_bounds__(kSplitThreads) void k_fa_split(FaArgs a) {
     const int j_end = a.causal ? min(n_kv, i + (n_kv - a.seq_q) + 1) : n_kv;
     // With a device-side length the plan was made for the capacity: the chunk is re-derived from the length
     // actually visible (whole batches, spread over all the planned splits; splits past it get no keys).
-    const int chunk = a.kv_len ? (n_kv + a.splits * KPB - 1) / (a.splits * KPB) * KPB : a.chunk;
+    int chunk = a.chunk;
+    if (a.kv_len) chunk = ceil_div_uniform(n_kv, a.splits * KPB) * KPB;
     const int j0 = split * chunk;
     const int j1 = min(j0 + chunk, j_end);
 
