@@ -92,6 +92,9 @@ def main():
                          "shapes): 'roofline' = the Q4_0 4096x14336 mat-vec, 'fa' = FA decode at --fa-ctx, "
                          "'decode' = the end-to-end 8B greedy decode")
     ap.add_argument("--fa-ctx", type=int, nargs="+", default=[512, 640, 2048, 8192, 32768])
+    ap.add_argument("--fa-fp16-only", action="store_true",
+                    help="with --only fa: the fp16 cache at --fa-ctx alone (no device-length or quantized-cache "
+                         "runs), so a profile of the run holds one configuration")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: this decode path runs on a "
@@ -130,8 +133,9 @@ def main():
         print(json.dumps({"only": "roofline", "roofline": roof, "calibration_copy_bytes": 32 << 20}))
         return
     if args.only == "fa":
-        rec = {"only": "fa", "fa_decode": measure_fa(torch, P, lib, timer, gen, args.fa_ctx)}
-        for kv_type in ("q8_0", "q4_0"):
+        rec = {"only": "fa", "fa_decode": measure_fa(torch, P, lib, timer, gen, args.fa_ctx,
+                                                     kvlen_runs=not args.fa_fp16_only)}
+        for kv_type in () if args.fa_fp16_only else ("q8_0", "q4_0"):
             rec[f"fa_decode_{kv_type}_kv"] = measure_fa_quant(torch, P, lib, synth, timer, gen, args.fa_ctx, kv_type)
         print(json.dumps(rec))
         return
@@ -239,7 +243,7 @@ def measure_roofline(torch, P, lib, timer, layers, x):
             "algorithmic_bytes": b, "avg_us": round(med, 3), "min_us": round(mn, 3)}
 
 
-def measure_fa(torch, P, lib, timer, gen, ctxs):
+def measure_fa(torch, P, lib, timer, gen, ctxs, kvlen_runs=True):
     """FA decode: 32/8 heads, d 128, 1 query row, causal; KV caches rotated beyond the Infinity Cache."""
     dev = torch.device("cuda")
     fa = {}
@@ -268,6 +272,9 @@ def measure_fa(torch, P, lib, timer, gen, ctxs):
     # A short visible length in a large cache (device-side length, plan made for the capacity): the kernels spread
     # the visible keys over every planned split, so this should cost what the same length costs on its own.
     cap, kvlen = 8192, {}
+    if not kvlen_runs:
+        return {"config": "32 q heads / 8 kv heads, d 128, 1 query row, causal, fp16 K/V, fp32 o + lse; split-K "
+                          "pass + LSE combine pass (2 launches, timed together)", "by_ctx": fa}
     p = P.AttnParams(n_head_q=32, n_head_kv=8, seq_q=1, seq_kv=cap, d_qk=128, d_v=128, causal=True)
     nsets = max(2, min(16, (600 << 20) // (2 * 8 * cap * 128 * 2)))
     caches = [(torch.randn(8 * cap * 128, device=dev, generator=gen).half(),
