@@ -10,13 +10,29 @@ namespace {
 
 // Q8_1 (qmv_model.cpp:60-68, quantize.cu:88-110): d = amax/127 (IEEE division), q = round(x/d) with ties
 // away from zero, s = fp16(sum of the original x), plus the exact integer sum of q for k-quant minima.
-// Grid (ceil(K/256), ncols); K % 32 == 0, so the lanes past K are whole 32-lane halves that exit together.
+// Each lane holds 8 consecutive elements and a quad of lanes one block (q8_1_quad: the reference's butterfly
+// order through DPP and in-lane adds, so no cross-lane shuffle through LDS). Grid (ceil(K/2048), ncols);
+// K % 32 == 0, so the lanes past K are whole quads that exit together. X16: x is 16-byte aligned (two 16-byte
+// loads per lane), else 8 dword loads.
+template <bool X16>
 __global__ __launch_bounds__(256) void k_quantize_q8_1(const float* __restrict__ x, int8_t* __restrict__ qs,
                                                        float4* __restrict__ ds, int K) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= K) return;
+    const int e0 = (blockIdx.x * 256 + threadIdx.x) * 8;
+    if (e0 >= K) return;
     const size_t col = blockIdx.y;
-    q8_1_store(x[col * K + i], i, qs + col * K, ds + col * (K / 32));
+    const float* src = x + col * K + e0;
+    float v[8];
+    if constexpr (X16) {
+        const float4 a = reinterpret_cast<const float4*>(src)[0], b = reinterpret_cast<const float4*>(src)[1];
+        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = src[e];
+    }
+    const Q81Quad r = q8_1_quad(v);
+    *reinterpret_cast<uint2*>(qs + col * K + e0) = make_uint2(r.q0, r.q1);
+    if ((e0 & 31) == 0)
+        ds[col * (K / 32) + e0 / 32] = make_float4(round_fp16(r.d), round_fp16(r.s), static_cast<float>(r.isum), 0.0f);
 }
 
 // h16 pre-pass (qmv_model.cpp:57-68; 0005 patch :185-207): s = amax, x^ = fp16(x/s) stored at the permuted
@@ -45,8 +61,11 @@ __global__ __launch_bounds__(256) void k_round_fp16(const float* __restrict__ x,
 }  // namespace
 
 hipError_t launch_quantize_q8_1(const float* x, int8_t* qs, float* ds, int K, int ncols, hipStream_t stream) {
-    const dim3 grid((K + 255) / 256, ncols);
-    hipLaunchKernelGGL(k_quantize_q8_1, grid, dim3(256), 0, stream, x, qs, reinterpret_cast<float4*>(ds), K);
+    const dim3 grid((K + 2047) / 2048, ncols);
+    if (reinterpret_cast<uintptr_t>(x) % 16 == 0)
+        hipLaunchKernelGGL(k_quantize_q8_1<true>, grid, dim3(256), 0, stream, x, qs, reinterpret_cast<float4*>(ds), K);
+    else
+        hipLaunchKernelGGL(k_quantize_q8_1<false>, grid, dim3(256), 0, stream, x, qs, reinterpret_cast<float4*>(ds), K);
     return hipGetLastError();
 }
 

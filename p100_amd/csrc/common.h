@@ -128,25 +128,6 @@ __device__ __forceinline__ float half_sum32(float v) {
     for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o);
     return v;
 }
-__device__ __forceinline__ int half_isum32(int v) {
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
-
-// Q8_1 of one activation element per lane, the 32 lanes of a wave half holding one whole block (element i of
-// the column, i % 32 == lane % 32) (qmv_model.cpp:60-68, quantize.cu:88-110): d = amax/127 (IEEE division),
-// q = round(x/d) with ties away from zero, s = fp16(butterfly sum of x), isum = the exact sum of q.
-__device__ __forceinline__ void q8_1_store(float v, int64_t i, int8_t* __restrict__ qs, float4* __restrict__ ds) {
-    const float amax = half_max32(fabsf(v));
-    const float d = amax / 127.0f;
-    const int q = amax == 0.0f ? 0 : static_cast<int>(roundf(v / d));
-    qs[i] = static_cast<int8_t>(q);
-    const float s = half_sum32(v);
-    const int isum = half_isum32(q);
-    if ((i & 31) == 0) ds[i / 32] = make_float4(round_fp16(d), round_fp16(s), static_cast<float>(isum), 0.0f);
-}
-
 // DPP exchanges inside a quad of lanes: the value of lane ^ 1 and of lane ^ 2.
 __device__ __forceinline__ int quad_xor1_i(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, true); }
 __device__ __forceinline__ int quad_xor2_i(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, true); }
@@ -173,7 +154,8 @@ __device__ __forceinline__ float norm_wave_total(float v) {
 }
 
 // Q8_1 of a 32-element block held by a quad of lanes, 8 consecutive elements per lane (lane t of the quad holds
-// elements 8t..8t+7), with the arithmetic of q8_1_store: d = amax/127 and q = round(x/d) (IEEE division), and
+// elements 8t..8t+7), with the reference's arithmetic (qmv_model.cpp:60-68, quantize.cu:88-110): d = amax/127 and
+// q = round(x/d) (IEEE division, ties away from zero), and
 // the sum s in the reference's butterfly order exactly (offsets 16 and 8 are the lane bits 1 and 0 of the quad,
 // exchanged by DPP; offsets 4, 2, 1 are inside the lane). Every lane gets d, s and isum; q holds its 8 codes as
 // two little-endian dwords.

@@ -498,7 +498,7 @@ __device__ __forceinline__ float wave_sum_rl(float v) {
 
 // Q8_1 of an output row held CPL consecutive columns per lane (the combine's layout), for a mat-vec that takes the
 // attention output next: element e of a 32-block sits in lane bits log2(CPL).. and in-lane bits below, and the
-// block sum follows the reference's butterfly order (offsets 16 .. 1; q8_1_store's arithmetic otherwise).
+// block sum follows the reference's butterfly order (offsets 16 .. 1; q8_1_quad's arithmetic otherwise).
 // One step of the butterfly over the 32 elements of a block held CPL per lane: element offset OFF is the lane
 // distance OFF / CPL when OFF >= CPL, else a distance inside the lane.
 template <int OFF, int CPL>
