@@ -202,7 +202,7 @@ int p1x_prepare_h16(const float* x, uint16_t* h, float* meta, int64_t K, int64_t
 size_t p1x_mul_mat_vec_workspace(int wtype, int64_t M, int64_t K, int64_t ncols, int act_mode) {
     if (K <= 0 || ncols <= 0 || M <= 0) return 0;
     if (act_mode == P1X_ACT_H16) return h16_bytes(K, ncols);
-    const bool fused = ncols <= 8 && K <= INT32_MAX && M <= INT32_MAX && !p1x::mmq_preferred(wtype, int(ncols), int(K)) &&
+    const bool fused = ncols <= 8 && K <= INT32_MAX && M <= INT32_MAX && !p1x::mmq_preferred(wtype, int(ncols), int(M), int(K)) &&
                        p1x::mmvq_fused_fits(int(ncols), int(M), int(K));
     return fused ? 0 : q8_1_bytes(K, ncols);
 }
@@ -216,7 +216,7 @@ int p1x_mul_mat_vec_q8_1(int wtype, const void* w, int64_t nb01, int64_t M, int6
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (ncols > 8 && !p1x::mmq_fits(int(M), nb01, int(K), int(ncols)))
         return fail(P1X_EUNSUPPORTED, "9..16 columns need the weights (M * nb01) within 2 GiB");
-    hipError_t e = p1x::mmq_preferred(wtype, int(ncols), int(K)) && p1x::mmq_fits(int(M), nb01, int(K), int(ncols))
+    hipError_t e = p1x::mmq_preferred(wtype, int(ncols), int(M), int(K)) && p1x::mmq_fits(int(M), nb01, int(K), int(ncols))
                        ? p1x::launch_mmq(wtype, int(ncols), w, nb01, int(M), int(K), qs, ds, y, group_sums, s)
                        : p1x::launch_mmvq(wtype, int(ncols), w, nb01, int(M), int(K), qs, ds, nullptr, y, group_sums, s);
     return e == hipSuccess ? P1X_OK : hip_fail(e, "mul_mat_vec_q8_1");
@@ -262,7 +262,7 @@ int p1x_mul_mat_vec(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K
             return fail(P1X_EUNSUPPORTED, "9..16 columns need the weights (M * nb01) within 2 GiB");
         hipError_t e = p1x::launch_quantize_q8_1(x, qs, ds, int(K), int(ncols), s);
         if (e != hipSuccess) return hip_fail(e, "quantize_q8_1");
-        e = p1x::mmq_preferred(wtype, int(ncols), int(K)) && p1x::mmq_fits(int(M), nb01, int(K), int(ncols))
+        e = p1x::mmq_preferred(wtype, int(ncols), int(M), int(K)) && p1x::mmq_fits(int(M), nb01, int(K), int(ncols))
                 ? p1x::launch_mmq(wtype, int(ncols), w, nb01, int(M), int(K), qs, ds, y, group_sums, s)
                 : p1x::launch_mmvq(wtype, int(ncols), w, nb01, int(M), int(K), qs, ds, nullptr, y, group_sums, s);
         return e == hipSuccess ? P1X_OK : hip_fail(e, "mul_mat_vec_q8_1");

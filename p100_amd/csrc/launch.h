@@ -58,7 +58,7 @@ hipError_t launch_mmvq_rope_kv(int type, const void* w, int64_t nb01, int M, int
 // prepared Q8_1 activation.
 constexpr int kMmqMaxCols = 16;
 bool mmq_supported(int type, int B);
-bool mmq_preferred(int type, int B, int K);  // the form chosen for B columns (always for B > 8)
+bool mmq_preferred(int type, int B, int M, int K);  // the form chosen for B columns (always for B > 8)
 bool mmq_fits(int M, int64_t nb01, int K, int B);  // weight and activation byte ranges within 32-bit buffer offsets
 hipError_t launch_mmq(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
                       float* y, int32_t* gs, hipStream_t stream);

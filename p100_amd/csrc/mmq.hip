@@ -50,7 +50,6 @@ struct MfmaW<Q8_0> {
 #ifndef P1X_MMQ_PAD
 #define P1X_MMQ_PAD 4
 #endif
-constexpr int kMmqWaves = 4;    // waves per work-group, each over a contiguous quarter of the K blocks
 constexpr int kStepBlocks = 8;  // K blocks per step (staged through LDS)
 
 // Buffer loads with a range check: offsets at or past the resource size read zeros and touch no memory, so the
@@ -75,8 +74,10 @@ struct MmqStage {
     float4 s[kStepBlocks][16];
 };
 
-template <int TYPE, bool SUMS>
-__global__ __launch_bounds__(64 * kMmqWaves) void k_mmq_mfma(const uint8_t* __restrict__ w, int64_t nb01, int M, int K,
+// NW waves per work-group, each over a contiguous share of the K blocks: 8 where the grid is small (M <= 8192, at
+// most 512 work-groups, so a CU holds one and 8 waves give each SIMD two), 4 above (more work-groups per CU).
+template <int TYPE, bool SUMS, int NW>
+__global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict__ w, int64_t nb01, int M, int K,
                                                             int B, const int8_t* __restrict__ xq,
                                                             const float4* __restrict__ xds, float* __restrict__ y,
                                                             int32_t* __restrict__ gs) {
@@ -85,13 +86,13 @@ __global__ __launch_bounds__(64 * kMmqWaves) void k_mmq_mfma(const uint8_t* __re
     constexpr int BB = W::kBytes;
     constexpr int NWL = (U * BB + 4 + 63) / 64;  // 16-byte loads per lane (4 lanes per row)
     constexpr int ROWDW = 16 * NWL + P1X_MMQ_PAD;  // staged dwords per row (padding spreads rows over LDS banks)
-    __shared__ MmqStage<ROWDW> stage[kMmqWaves];
-    __shared__ float red[kMmqWaves - 1][4][64];  // partial tiles of waves 1.., result-major (conflict-free)
+    __shared__ MmqStage<ROWDW> stage[NW];
+    __shared__ float red[NW - 1][4][64];  // partial tiles of waves 1.., result-major (conflict-free)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, i16 = lane & 15;
     const int m0 = blockIdx.x * 16;
     const int nblk = K / 32;
-    const int per = (nblk + kMmqWaves - 1) / kMmqWaves;
+    const int per = (nblk + NW - 1) / NW;
     const int b0 = min(nblk, wave * per), b1 = min(nblk, b0 + per);
     MmqStage<ROWDW>& st = stage[wave];
 
@@ -206,7 +207,7 @@ __global__ __launch_bounds__(64 * kMmqWaves) void k_mmq_mfma(const uint8_t* __re
     __syncthreads();
     if (wave != 0 || i16 >= B) return;
 #pragma unroll
-    for (int k = 0; k < kMmqWaves - 1; ++k)
+    for (int k = 0; k < NW - 1; ++k)
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[r] += red[k][r][lane];
     const int mrow = m0 + 4 * g;
@@ -228,11 +229,15 @@ bool mmq_fits(int M, int64_t nb01, int K, int B) {
     return int64_t(M) * nb01 + 3 <= int64_t(kOob) && int64_t(B) * K <= int64_t(kOob) &&
            int64_t(B) * (K / 32) * 16 <= int64_t(kOob);
 }
-// From 9 columns always; also q8_0 rows longer than 8192 at 7-8 columns, where the dot4 kernel's LDS-staged
-// activation (7-8 x 14336 x 1.5 bytes per work-group) outweighs the matrix-core form (q8_0 4096x14336, graph period:
-// 8 columns 43.2 -> 35.7 us, 7 columns 36.1 -> 35.8; q4_0 and K <= 8192 stay faster on dot4 at <= 8 columns).
-bool mmq_preferred(int type, int B, int K) {
-    return mmq_supported(type, B) && (B >= P1X_MMQ_MIN_COLS || (type == Q8_0 && B >= 7 && K > 8192));
+// From 9 columns always; also rows longer than 8192 on at most 8192 rows (the 8-wave form) from 5 columns for q8_0
+// and 7 for q4_0, where the dot4 kernel's LDS-staged activation (B x 14336 x 1.5 bytes per work-group) outweighs
+// it (4096x14336, graph period, dot4 at 5 / 6 / 7 / 8 columns against the matrix-core form at any count: q8_0
+// 30.4 / 33.8 / 36.1 / 43.2 against 25.9 us; q4_0 20.3 / 23.2 / 26.8 / 29.5 against 22.6 us). K <= 8192 stays on
+// dot4 up to 8 columns (e.g. 4096x4096 at 8 columns 8.5 against 9.5 us).
+bool mmq_preferred(int type, int B, int M, int K) {
+    if (!mmq_supported(type, B)) return false;
+    if (B >= P1X_MMQ_MIN_COLS) return true;
+    return K > 8192 && M <= 8192 && B >= (type == Q8_0 ? 5 : 7);
 }
 
 hipError_t launch_mmq(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
@@ -241,7 +246,12 @@ hipError_t launch_mmq(int type, int B, const void* w, int64_t nb01, int M, int K
     const auto* wb = static_cast<const uint8_t*>(w);
     const auto* d4 = reinterpret_cast<const float4*>(xds);
 #define P1X_MMQ(T, S) \
-    hipLaunchKernelGGL((k_mmq_mfma<T, S>), grid, dim3(64 * kMmqWaves), 0, stream, wb, nb01, M, K, B, xq, d4, y, gs)
+    do {                                                                                                           \
+        if (M <= 8192)                                                                                             \
+            hipLaunchKernelGGL((k_mmq_mfma<T, S, 8>), grid, dim3(512), 0, stream, wb, nb01, M, K, B, xq, d4, y, gs); \
+        else                                                                                                       \
+            hipLaunchKernelGGL((k_mmq_mfma<T, S, 4>), grid, dim3(256), 0, stream, wb, nb01, M, K, B, xq, d4, y, gs); \
+    } while (0)
     if (type == Q4_0) {
         if (gs) P1X_MMQ(Q4_0, true);
         else P1X_MMQ(Q4_0, false);

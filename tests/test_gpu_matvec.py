@@ -165,8 +165,9 @@ def test_many_columns_parity(orc, gpu, tname):
     import p100_amd as P
 
     t = orc.TYPES[tname]
-    for k, rows in ((32, 17), (64, 33), (96, 16), (96, 17), (4128, 17), (4096, 17), (14336, 33), (4096, 4096)):
-        for ncols in ((9, 12, 16) if rows < 4096 else (16,)):
+    for k, rows in ((32, 17), (64, 33), (96, 16), (96, 17), (4128, 17), (4096, 17), (14336, 33), (4096, 4096),
+                    (64, 8232)):
+        for ncols in ((9, 12, 16) if rows < 4096 else (16,)):  # up to 8192 rows 8 waves per work-group, then 4
             w, x = make_case(orc, t, k, rows, ncols, seed=900 + k + rows + ncols)
             y, sums = P.mul_mat_vec(t, to_dev(w), rows, k, to_dev(x), act="q8_1", group_sums=True)
             check_matvec(orc, t, w, x, y.cpu().numpy(), sums.cpu().numpy(), "q81")
@@ -176,14 +177,15 @@ def test_many_columns_parity(orc, gpu, tname):
             assert (y3.view(np.uint32) == y2.view(np.uint32)).all()
 
 
-def test_q8_0_long_rows_seven_eight_columns(orc, gpu):
-    """q8_0 rows longer than 8192 at 7 and 8 columns take the matrix-core form: sums bit-exact, FP32 within the
-    bars, the same bits through the fp32 op and a prepared activation."""
+@pytest.mark.parametrize("tname", ["q4_0", "q8_0"])
+def test_long_rows_five_to_eight_columns(orc, gpu, tname):
+    """Rows longer than 8192 at 5-8 columns (the matrix-core form from 5 columns for q8_0 and 7 for q4_0, dot4
+    below): sums bit-exact, FP32 within the bars, the same bits through the fp32 op and a prepared activation."""
     import p100_amd as P
 
-    t = orc.TYPES["q8_0"]
+    t = orc.TYPES[tname]
     for k, rows in ((8224, 19), (14336, 40)):
-        for ncols in (7, 8):
+        for ncols in (5, 6, 7, 8):
             w, x = make_case(orc, t, k, rows, ncols, seed=700 + k + rows + ncols)
             y, sums = P.mul_mat_vec(t, to_dev(w), rows, k, to_dev(x), act="q8_1", group_sums=True)
             check_matvec(orc, t, w, x, y.cpu().numpy(), sums.cpu().numpy(), "q81")
