@@ -790,7 +790,7 @@ hipError_t launch_mmvr(const MmvrPlan& p, const uint8_t* w, int64_t nb01, int M,
     return hipErrorInvalidValue;
 }
 
-// 2..4 activation columns (q4_0 / q8_0, prepared Q8_1): k_mmvr with B columns. Each thread holds its units' Q8_1
+// 2..8 activation columns (q4_0 / q8_0, prepared Q8_1): k_mmvr with B columns. Each thread holds its units' Q8_1
 // blocks of every column (B x UPT blocks) and each decoded weight unit serves the B columns; rows are stored as
 // they are (y[c][r]).
 template <int TYPE, int NWK, int UPT, int R, int B, bool SUMS>
@@ -865,12 +865,24 @@ __global__ __launch_bounds__(256) void k_mmvr_cols(const uint8_t* __restrict__ w
     }
 }
 
-// Row-group shape of k_mmvr_cols (measured on the Llama-3-8B matrices at 2..4 columns against k_mmvq): rows of up
-// to 128 units take 2 waves x 1 unit x 2 rows where that is faster (M <= 4096, 2 columns, or q4_0 at 3 columns);
-// up to 256 units 2 x 2 x 2; up to 512 units 4 x 2 x 4 (4 x 2 x 2 for q4_0 at 2 columns). Otherwise k_mmvq.
+// Row-group shape of k_mmvr_cols (measured on the Llama-3-8B matrices at 2..8 columns against k_mmvq): at 2..4
+// columns, rows of up to 128 units take 2 waves x 1 unit x 2 rows where that is faster (M <= 4096, 2 columns, or
+// q4_0 at 3 columns); up to 256 units 2 x 2 x 2; up to 512 units 4 x 2 x 4 (4 x 2 x 2 for q4_0 at 2 columns). At
+// 5..8 columns only rows of up to 128 units: q4_0 2 x 1 x 2 (x 4 above 8192 rows); q8_0 up to 8192 rows, 2 rows
+// (4 from 7 columns above 2048 rows), except 5..6 columns on 2049..4096 rows. Otherwise k_mmvq.
 bool mmvr_cols_plan(int type, int M, int K, int B, MmvrPlan& p) {
-    if (!P1X_MMVR_ENABLE || (type != Q4_0 && type != Q8_0) || B < 2 || B > 4) return false;
+    if (!P1X_MMVR_ENABLE || (type != Q4_0 && type != Q8_0) || B < 2 || B > 8) return false;
     const int units = K / 32;
+    if (B > 4) {  // 5..8 columns, rows of at most 4096 elements: 2 waves x 1 unit, 2 or 4 rows
+        if (units > 128) return false;
+        if (type == Q4_0) {
+            p = {2, 1, M > 8192 ? 4 : 2};
+        } else {
+            if (M > 8192 || (B <= 6 && M > 2048 && M <= 4096)) return false;
+            p = {2, 1, B >= 7 && M > 2048 ? 4 : 2};
+        }
+        return true;
+    }
     if (units <= 128) {
         if (!(M <= 4096 || B == 2 || (type == Q4_0 && B == 3))) return false;
         p = {2, 1, 2};
@@ -903,6 +915,8 @@ hipError_t launch_mmvr_cols(const MmvrPlan& p, int B, const uint8_t* w, int64_t 
     P1X_COLS_B(2, 2, 2)
     P1X_COLS_B(4, 2, 2)
     P1X_COLS_B(4, 2, 4)
+    P1X_COLS(2, 1, 2, 5) P1X_COLS(2, 1, 2, 6) P1X_COLS(2, 1, 2, 7) P1X_COLS(2, 1, 2, 8)
+    P1X_COLS(2, 1, 4, 5) P1X_COLS(2, 1, 4, 6) P1X_COLS(2, 1, 4, 7) P1X_COLS(2, 1, 4, 8)
 #undef P1X_COLS_B
 #undef P1X_COLS
     return hipErrorInvalidValue;

@@ -266,15 +266,15 @@ def test_one_column_register_kernel(orc, gpu, tname):
             assert (y3.view(np.uint32) == y2.view(np.uint32)).all(), (rows, k)
 
 
-COLUMN_REGISTER_CASES = [(17, 2048), (1029, 4096), (4099, 4096), (37, 6144), (41, 8192), (45, 14336),
-                         (43, 16384), (19, 16416)]
+COLUMN_REGISTER_CASES = [(17, 2048), (1029, 4096), (2100, 4096), (4099, 4096), (8200, 4096), (37, 6144), (41, 8192),
+                         (45, 14336), (43, 16384), (19, 16416)]
 
 
-@pytest.mark.parametrize("ncols", [2, 3, 4])
+@pytest.mark.parametrize("ncols", [2, 3, 4, 5, 6, 7, 8])
 @pytest.mark.parametrize("tname", ["q4_0", "q8_0"])
 def test_column_register_kernel(orc, gpu, tname, ncols):
-    """2..4 columns on a prepared Q8_1 activation (the register-resident kernel where its plan applies, the
-    streaming kernel elsewhere): int32 group sums bit-exact per column, FP32 within the bars, the group-sum export
+    """2..8 columns on a prepared Q8_1 activation (the register-resident kernel where its plan applies, the
+    streaming or matrix-core kernel elsewhere): int32 group sums bit-exact per column, FP32 within the bars, the group-sum export
     leaving the FP32 result unchanged, and a padded row stride."""
     import p100_amd as P
 
