@@ -926,16 +926,27 @@ template <int TYPE, int B>
 hipError_t launch_b(const uint8_t* w, int64_t nb01, int M, int K, int rw, const int8_t* xq, const float4* xds,
                     const float* x, float* y, int32_t* gs, hipStream_t stream) {
     if (gs) rw = 1;  // the group-sum export is a check path: one row per wave
+    // The single-launch form quantizes x itself; it serves one column (p1x_mul_mat_vec takes the Q8_1 pass and the
+    // prepared kernels from two columns on).
+    if (x && B != 1) return hipErrorInvalidValue;
     const dim3 grid((M + 4 * rw - 1) / (4 * rw));
     const size_t lds = size_t(48) * B * (K / 32);
     const bool use_lds = lds <= 65536;
 #define P1X_RW(R)                                                                                                  \
     if (rw == R) {                                                                                                 \
-        if (x && gs)                                                                                               \
-            hipLaunchKernelGGL((k_mmvq_fx<TYPE, B, R, true>), grid, dim3(256), lds, stream, w, nb01, M, K, x, y, gs); \
-        else if (x)                                                                                                \
-            hipLaunchKernelGGL((k_mmvq_fx<TYPE, B, R, false>), grid, dim3(256), lds, stream, w, nb01, M, K, x, y, gs); \
-        else if (gs && use_lds)                                                                                    \
+        if constexpr (B == 1) {                                                                                    \
+            if (x && gs) {                                                                                         \
+                hipLaunchKernelGGL((k_mmvq_fx<TYPE, B, R, true>), grid, dim3(256), lds, stream, w, nb01, M, K, x, y, \
+                                   gs);                                                                            \
+                return hipGetLastError();                                                                          \
+            }                                                                                                      \
+            if (x) {                                                                                               \
+                hipLaunchKernelGGL((k_mmvq_fx<TYPE, B, R, false>), grid, dim3(256), lds, stream, w, nb01, M, K, x, y, \
+                                   gs);                                                                            \
+                return hipGetLastError();                                                                          \
+            }                                                                                                      \
+        }                                                                                                          \
+        if (gs && use_lds)                                                                                         \
             hipLaunchKernelGGL((k_mmvq<TYPE, B, R, true, true>), grid, dim3(256), lds, stream, w, nb01, M, K, xq, xds, y, \
                                gs);                                                                                \
         else if (gs)                                                                                               \
