@@ -202,10 +202,10 @@ int p1x_prepare_h16(const float* x, uint16_t* h, float* meta, int64_t K, int64_t
 size_t p1x_mul_mat_vec_workspace(int wtype, int64_t M, int64_t K, int64_t ncols, int act_mode) {
     if (K <= 0 || ncols <= 0 || M <= 0) return 0;
     if (act_mode == P1X_ACT_H16) return h16_bytes(K, ncols);
-    // One launch (each work-group quantizes x itself) for one column where that fits; from two columns the Q8_1
-    // pass plus the register-resident kernel is as fast or faster (1024x4096 at 2 columns 5.7 -> 4.6 us, 4096x4096
-    // unchanged).
-    const bool fused = ncols == 1 && K <= INT32_MAX && M <= INT32_MAX &&
+    // One launch (each work-group quantizes x itself) for one column where that fits (mmvq_fused_fits); from two
+    // columns the Q8_1 pass plus the register-resident kernel is as fast or faster (1024x4096 at 2 columns
+    // 5.7 -> 4.6 us, 4096x4096 unchanged).
+    const bool fused = K <= INT32_MAX && M <= INT32_MAX &&
                        !p1x::mmq_preferred(wtype, int(ncols), int(M), int(K)) &&
                        p1x::mmvq_fused_fits(int(ncols), int(M), int(K));
     return fused ? 0 : q8_1_bytes(K, ncols);

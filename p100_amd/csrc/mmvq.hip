@@ -994,10 +994,11 @@ int mmvq_rows_per_wave(int M, int B, bool fused) {
     return 1;
 }
 
-// The single-launch form (x quantized into LDS by each work-group) when its 48 bytes per block and column fit in
-// 64 KiB of LDS and the repeated quantization (work-groups x B x K elements) stays small next to the weight
+// The single-launch form (x quantized into LDS by each work-group), for one column, when its 48 bytes per block
+// fit in 64 KiB of LDS and the repeated quantization (work-groups x K elements) stays small next to the weight
 // stream; otherwise the activation goes through p1x_quantize_q8_1 and a workspace.
 bool mmvq_fused_fits(int B, int M, int K) {
+    if (B != 1) return false;
     const int rw = mmvq_rows_per_wave(M, B, true);
     const long wgs = (M + 4L * rw - 1) / (4L * rw);  // every work-group quantizes all B x K elements
     return size_t(48) * B * (K / 32) <= 65536 && wgs * K * B <= P1X_MMVQ_FUSE_MAX;
