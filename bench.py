@@ -87,10 +87,12 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline and roofline only")
-    ap.add_argument("--only", choices=("roofline", "fa", "decode"), default=None,
+    ap.add_argument("--only", choices=("roofline", "fa", "decode", "cols"), default=None,
                     help="run one measurement alone (for profiler runs whose per-kernel averages must not mix "
                          "shapes): 'roofline' = the Q4_0 4096x14336 mat-vec, 'fa' = FA decode at --fa-ctx, "
-                         "'decode' = the end-to-end 8B greedy decode")
+                         "'decode' = the end-to-end 8B greedy decode, 'cols' = the Q4_0 4096x14336 mat-vec on a "
+                         "prepared Q8_1 activation of --cols columns")
+    ap.add_argument("--cols", type=int, nargs="+", default=[4, 16])
     ap.add_argument("--fa-ctx", type=int, nargs="+", default=[512, 640, 2048, 8192, 32768])
     ap.add_argument("--fa-fp16-only", action="store_true",
                     help="with --only fa: the fp16 cache at --fa-ctx alone (no device-length or quantized-cache "
@@ -110,6 +112,30 @@ def main():
     dev = torch.device("cuda")
     if args.only == "decode":
         print(json.dumps({"only": "decode", "decode_8b": measure_decode(torch)}))
+        return
+    if args.only == "cols":
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(77)
+        M, K = 4096, 14336
+        wsets = [synth.random_weights(P.Q4_0, M, K, generator=gen) for _ in range(8)]
+        timer = GraphTimer(torch)
+        rec = {}
+        for n in args.cols:
+            q = P.quantize_q8_1(torch.randn((n, K), device=dev, generator=gen))
+            y = torch.empty((n, M), device=dev)
+
+            def call(i, s, q=q, y=y, n=n):
+                rc = lib.p1x_mul_mat_vec_q8_1(P.Q4_0, C.c_void_p(wsets[i % 8].data_ptr()), K // 32 * 18, M, K,
+                                              C.c_void_p(q.qs.data_ptr()), C.c_void_p(q.ds.data_ptr()), n,
+                                              C.c_void_p(y.data_ptr()), None, s)
+                if rc:
+                    raise RuntimeError(lib.p1x_last_error().decode())
+
+            med, mn, _ = timer.period_us(call, n=32)
+            b = matvec_bytes(P.Q4_0, M, K, n)
+            rec[str(n)] = {"us": round(med, 3), "min_us": round(mn, 3), "gbs": round(b / (med * 1e-6) / 1e9, 1)}
+            log(f"[bench] Q4_0 {M}x{K} at {n} columns (prepared Q8_1): {med:.2f} us")
+        print(json.dumps({"only": "cols", "q4_0_4096x14336_prepared": rec}))
         return
     log(f"[bench] {torch.cuda.get_device_name(0)}; building {args.layers} Q4_0 layers")
     gen = torch.Generator(device="cuda")
