@@ -17,8 +17,9 @@
 // moves; probabilities are 2^(x - ref) <= 2^kTau, and the groups' partial sums merge by plain addition (DPP
 // inside a 16-lane row, then LDS across rows and waves); the work-group writes one unnormalised partial
 // (O, max, sum) per head.
-// Pass 2 (k_fa_combine): one wave per output row rebases every split's partial to the common max and sums
-// (one round of loads per 32 splits). With a single split, pass 1 writes O and LSE itself and pass 2 is skipped.
+// Pass 2 (k_fa_combine): one single-wave work-group per output row rebases every split's partial to the common max
+// and sums (one round of loads per 8, 16 or 32 splits, sized to the plan). With a single split, pass 1 writes O
+// and LSE itself and pass 2 is skipped.
 // (A single launch, where the last work-group to arrive combines, needs an agent-scope release per work-group:
 // each one writes back the XCD's L2, and one per work-group alone costs more than the second launch.)
 #include <type_traits>

@@ -5,16 +5,17 @@
 // (the reference's per-block integer dot products, bit for bit); each block's sums are then scaled in FP32 with
 // the same per-block formula as the dot4 path (src/reference/qmv_model.cpp q81 path: q4_0 d*(dot*d8 - 8*s8),
 // q8_0 d*d8*dot). Where the dot4 path re-reads every activation column for every weight row, here one wave
-// serves 16 rows per activation read, which is what makes 4..16 columns cheap.
+// serves 16 rows per activation read, which is what makes many columns cheap (used from 9 columns, and from 5-7
+// on rows longer than 8192).
 //
 // Lane layout of v_mfma_i32_16x16x32_i8 (checked on the device): A (16 x 32) lane l holds row l % 16, elements
 // 8 (l / 16) .. + 7; B (32 x 16) lane l holds column l % 16, the same elements; D (16 x 16) lane l holds rows
 // 4 (l / 16) .. + 3 of column l % 16. A = weights, B = activation, so a lane's four results share its own
-// activation column (one scale load) and need the weight scales of four rows (four ds_bpermute).
+// activation column (one scale load) and need the weight scales of four rows (read from the staged rows in LDS).
 //
-// Work-group: 16 weight rows, P1X_MMQ_WAVES waves, each over a contiguous share of the K blocks, P1X_MMQ_UNROLL
-// blocks per step with the next step's loads in flight; the partial 16 x 16 tiles are added in LDS in a fixed
-// order (deterministic, no workspace). Grid: ceil(M / 16).
+// Work-group: 16 weight rows, 8 waves (up to 8192 rows) or 4, each over a contiguous share of the K blocks, 8
+// blocks per step staged through the wave's own LDS area with the next step's loads in flight; the partial
+// 16 x 16 tiles are added in LDS in a fixed order (deterministic, no workspace). Grid: ceil(M / 16).
 #include "common.h"
 #include "launch.h"
 

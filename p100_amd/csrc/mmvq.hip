@@ -15,7 +15,10 @@
 // cross-row swizzles; four independent waves form a 256-thread work-group.
 //
 // One column of q4_0 / q8_0 on a prepared activation takes k_mmvr instead: the activation is held in registers by
-// row-groups of 1-4 waves that split K, so there is no LDS copy and no barrier ahead of the weight stream.
+// row-groups of 1-4 waves that split K, so there is no LDS copy and no barrier ahead of the weight stream. Its
+// activation can also be the RMSNorm of the residual stream, normalized and quantized by every work-group
+// (SrcNorm), and its store step can add into a residual, apply RoPE and append to the KV cache, or write SwiGLU.
+// 2..8 columns of q4_0 / q8_0 take k_mmvr_cols where its plan applies (mmvr_cols_plan).
 #include "common.h"
 #include "launch.h"
 
@@ -32,7 +35,7 @@
 #define P1X_MMVQ_MIN_WAVES_MB 4096  // the same for several activation columns (rows per wave amortise their reads)
 #endif
 #ifndef P1X_MMVQ_FUSE_MAX
-#define P1X_MMVQ_FUSE_MAX (1L << 21)  // single launch while work-groups x B x K stays at or below this
+#define P1X_MMVQ_FUSE_MAX (1L << 21)  // single launch (one column) while work-groups x K stays at or below this
 #endif
 #ifndef P1X_MMVQ_HOIST
 #define P1X_MMVQ_HOIST 1  // prepared activation: first weight pass requested before the LDS copy
