@@ -45,6 +45,12 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def ok(lib, rc, what):
+    """Every timed C-ABI call is checked: a rejected call enqueues nothing, and an empty replay must not be timed."""
+    if rc:
+        raise RuntimeError(f"{what}: p1x error {rc}: {lib.p1x_last_error().decode()}")
+
+
 class GraphTimer:
     """Per-launch period of `n` back-to-back launches captured in one HIP graph (launch i gets index i, so the
     callee can rotate buffers), timed with HIP events around replays on the current stream."""
@@ -245,9 +251,9 @@ def measure_roofline(torch, P, lib, timer, layers, x):
 
     def down(i, s):
         w = layers[i % len(layers)]["down"]
-        lib.p1x_mul_mat_vec_q8_1(P.Q4_0, C.c_void_p(w.data_ptr()), 14336 // 32 * 18, 4096, 14336,
-                                 C.c_void_p(q81.qs.data_ptr()), C.c_void_p(q81.ds.data_ptr()), 1,
-                                 C.c_void_p(y.data_ptr()), None, s)
+        ok(lib, lib.p1x_mul_mat_vec_q8_1(P.Q4_0, C.c_void_p(w.data_ptr()), 14336 // 32 * 18, 4096, 14336,
+                                         C.c_void_p(q81.qs.data_ptr()), C.c_void_p(q81.ds.data_ptr()), 1,
+                                         C.c_void_p(y.data_ptr()), None, s), "roofline mat-vec")
 
     med, mn, _ = timer.period_us(down)
     b = matvec_bytes(P.Q4_0, 4096, 14336, 1)
@@ -285,9 +291,10 @@ def measure_fa(torch, P, lib, timer, gen, ctxs, kvlen_runs=True):
 
         def call(i, s, p=p, caches=caches, q=q, o=o, lse=lse, fws=fws):
             k, v = caches[i % len(caches)]
-            lib.p1x_flash_attn_decode(C.byref(p), C.c_void_p(q.data_ptr()), C.c_void_p(k.data_ptr()),
-                                      C.c_void_p(v.data_ptr()), None, None, C.c_void_p(o.data_ptr()),
-                                      C.c_void_p(lse.data_ptr()), C.c_void_p(fws.data_ptr()), fws.numel() * 4, s)
+            ok(lib, lib.p1x_flash_attn_decode(C.byref(p), C.c_void_p(q.data_ptr()), C.c_void_p(k.data_ptr()),
+                                              C.c_void_p(v.data_ptr()), None, None, C.c_void_p(o.data_ptr()),
+                                              C.c_void_p(lse.data_ptr()), C.c_void_p(fws.data_ptr()),
+                                              fws.numel() * 4, s), "flash_attn_decode")
 
         med, mn, _ = timer.period_us(call, n=32)
         b = fa_bytes(32, 8, ctx, 128)
@@ -315,10 +322,11 @@ def measure_fa(torch, P, lib, timer, gen, ctxs, kvlen_runs=True):
 
         def call(i, s):
             k, v = caches[i % len(caches)]
-            lib.p1x_flash_attn_decode_kvlen(C.byref(p), C.c_void_p(q.data_ptr()), C.c_void_p(k.data_ptr()),
-                                            C.c_void_p(v.data_ptr()), None, None, C.c_void_p(n_dev.data_ptr()),
-                                            C.c_void_p(o.data_ptr()), C.c_void_p(lse.data_ptr()),
-                                            C.c_void_p(fws.data_ptr()), fws.numel() * 4, s)
+            ok(lib, lib.p1x_flash_attn_decode_kvlen(C.byref(p), C.c_void_p(q.data_ptr()), C.c_void_p(k.data_ptr()),
+                                                    C.c_void_p(v.data_ptr()), None, None,
+                                                    C.c_void_p(n_dev.data_ptr()), C.c_void_p(o.data_ptr()),
+                                                    C.c_void_p(lse.data_ptr()), C.c_void_p(fws.data_ptr()),
+                                                    fws.numel() * 4, s), "flash_attn_decode_kvlen")
 
         med, mn, _ = timer.period_us(call, n=32)
         kvlen[str(n)] = {"us": round(med, 3), "min_us": round(mn, 3)}
@@ -348,9 +356,11 @@ def measure_fa_quant(torch, P, lib, synth, timer, gen, ctxs, kv_type):
 
         def call(i, s, p=p, caches=caches, q=q, o=o, lse=lse, fws=fws):
             k, v = caches[i % len(caches)]
-            lib.p1x_flash_attn_decode_quant(C.byref(p), t, C.c_void_p(q.data_ptr()), C.c_void_p(k.data_ptr()),
-                                            C.c_void_p(v.data_ptr()), None, None, None, C.c_void_p(o.data_ptr()),
-                                            C.c_void_p(lse.data_ptr()), C.c_void_p(fws.data_ptr()), fws.numel() * 4, s)
+            ok(lib, lib.p1x_flash_attn_decode_quant(C.byref(p), t, C.c_void_p(q.data_ptr()),
+                                                    C.c_void_p(k.data_ptr()), C.c_void_p(v.data_ptr()), None, None,
+                                                    None, C.c_void_p(o.data_ptr()), C.c_void_p(lse.data_ptr()),
+                                                    C.c_void_p(fws.data_ptr()), fws.numel() * 4, s),
+               "flash_attn_decode_quant")
 
         med, mn, _ = timer.period_us(call, n=32)
         b = 2 * 8 * ctx * row + 32 * 128 * 4 * 2  # quantized K and V once per KV head, q and o in f32
@@ -372,13 +382,14 @@ def extra_measurements(torch, P, lib, synth, timer, gen, layers, xs, ctxs):
 
     def quant(K, s):
         qs, ds = acts[K]
-        lib.p1x_quantize_q8_1(C.c_void_p(xs[K].data_ptr()), C.c_void_p(qs.data_ptr()), C.c_void_p(ds.data_ptr()),
-                              K, 1, s)
+        ok(lib, lib.p1x_quantize_q8_1(C.c_void_p(xs[K].data_ptr()), C.c_void_p(qs.data_ptr()),
+                                      C.c_void_p(ds.data_ptr()), K, 1, s), "quantize_q8_1")
 
     def mv(w, M, K, y, s):
         qs, ds = acts[K]
-        lib.p1x_mul_mat_vec_q8_1(P.Q4_0, C.c_void_p(w.data_ptr()), K // 32 * 18, M, K, C.c_void_p(qs.data_ptr()),
-                                 C.c_void_p(ds.data_ptr()), 1, C.c_void_p(y.data_ptr()), None, s)
+        ok(lib, lib.p1x_mul_mat_vec_q8_1(P.Q4_0, C.c_void_p(w.data_ptr()), K // 32 * 18, M, K,
+                                         C.c_void_p(qs.data_ptr()), C.c_void_p(ds.data_ptr()), 1,
+                                         C.c_void_p(y.data_ptr()), None, s), "mul_mat_vec_q8_1")
 
     def shared_step(i, s):
         L = layers[i % len(layers)]
@@ -412,9 +423,9 @@ def extra_measurements(torch, P, lib, synth, timer, gen, layers, xs, ctxs):
                 wsb = torch.empty(wsz, dtype=torch.uint8, device=dev)
 
                 def call(i, s, wsets=wsets, x=x, y=y, wsb=wsb, wsz=wsz, M=M, K=K, n=n, wtype=wtype, rb=rb):
-                    lib.p1x_mul_mat_vec(wtype, C.c_void_p(wsets[i % len(wsets)].data_ptr()), rb, M, K, 0,
-                                        C.c_void_p(x.data_ptr()), n, C.c_void_p(y.data_ptr()), None,
-                                        C.c_void_p(wsb.data_ptr()), wsz, s)
+                    ok(lib, lib.p1x_mul_mat_vec(wtype, C.c_void_p(wsets[i % len(wsets)].data_ptr()), rb, M, K, 0,
+                                                C.c_void_p(x.data_ptr()), n, C.c_void_p(y.data_ptr()), None,
+                                                C.c_void_p(wsb.data_ptr()), wsz, s), "mul_mat_vec")
 
                 med, _, _ = timer.period_us(call, n=32)
                 b = matvec_bytes(wtype, M, K, n)

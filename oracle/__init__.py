@@ -73,7 +73,7 @@ class RowResult(C.Structure):
 
 def build(force: bool = False) -> None:
     """Compile liboracle.so (and the reference build when the reference checkout is present)."""
-    if force or not LIB_PATH.exists():
+    if force or not LIB_PATH.exists() or not (HERE / "libcpu_ggml.so").exists():
         subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
 
 
@@ -107,6 +107,7 @@ def _load():
         "orc_mul_mat_vec": (C.c_int, [C.c_int, u8p, C.c_int64, C.c_int64, C.c_int64, f32p, C.c_int64, C.c_int,
                                       f32p, C.c_void_p, C.c_int]),
         "orc_quantize": (C.c_int, [C.c_int, f32p, C.c_int64, u8p]),
+        "orc_weight_norms": (C.c_int, [C.c_int, u8p, C.c_int64, C.c_int64, C.c_int64, f64p, C.c_int]),
         "orc_attn_validate": (C.c_int, [C.POINTER(AttnParams)]),
         "orc_attention_reference": (C.c_int, [C.POINTER(AttnParams), C.c_void_p, C.c_void_p, C.c_void_p,
                                               C.c_void_p, C.c_void_p, C.c_void_p]),
@@ -242,6 +243,16 @@ def mul_mat_vec(wtype, w, M, K, x, mode="q81", nb01=None, want_sums=False, nthre
     return (y, sums) if want_sums else y
 
 
+def weight_norms(wtype, w, M, K, nb01=None, nthreads=0):
+    """||deq(w_row)|| (FP64) of every row: evaluate_row's weight_norm for a whole matrix."""
+    nb, bb = BLOCK[wtype]
+    nb01 = nb01 if nb01 is not None else K // nb * bb
+    w = np.ascontiguousarray(w, np.uint8).ravel()
+    out = np.empty(M, np.float64)
+    _check(lib().orc_weight_norms(wtype, w, nb01, M, K, out, nthreads))
+    return out
+
+
 def quantize(wtype, x):
     x = np.ascontiguousarray(x, np.float32)
     nb, bb = BLOCK[wtype]
@@ -277,6 +288,60 @@ def fa_decode_f32(p: AttnParams, q, k16, v16, mask=None, nthreads=0):
     _check(lib().orc_fa_decode_f32(C.byref(p), np.ascontiguousarray(q, np.float32),
                                    np.ascontiguousarray(k16, np.uint16), np.ascontiguousarray(v16, np.uint16),
                                    _ptr(m), o, _ptr(lse), nthreads))
+    return o, lse
+
+
+# ---------------------------------------------------------------- timed CPU baseline (cpu_ggml.cpp)
+CPU_GGML_PATH = HERE / "libcpu_ggml.so"
+_cpu = None
+
+
+def _cpu_lib():
+    global _cpu
+    if _cpu is None:
+        if not CPU_GGML_PATH.exists():
+            raise FileNotFoundError(f"{CPU_GGML_PATH} is not built (run make -C oracle)")
+        L = C.CDLL(str(CPU_GGML_PATH))
+        L.cpu_ggml_uses_vnni.restype, L.cpu_ggml_uses_vnni.argtypes = C.c_int, []
+        L.cpu_ggml_force_avx2.restype, L.cpu_ggml_force_avx2.argtypes = None, [C.c_int]
+        L.cpu_ggml_mul_mat_q4_0.restype = C.c_int
+        L.cpu_ggml_mul_mat_q4_0.argtypes = [u8p, C.c_int64, C.c_int64, C.c_int64, f32p, C.c_int64, f32p, C.c_int]
+        L.cpu_ggml_fa_decode.restype = C.c_int
+        L.cpu_ggml_fa_decode.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, f32p, u16p, u16p, f32p,
+                                         f32p, C.c_int]
+        _cpu = L
+    return _cpu
+
+
+def cpu_uses_vnni() -> bool:
+    return bool(_cpu_lib().cpu_ggml_uses_vnni())
+
+
+def cpu_force_avx2(on: bool) -> None:
+    """Run the AVX2 block dot even where AVX-512 VNNI exists (both kernels are tested)."""
+    _cpu_lib().cpu_ggml_force_avx2(int(on))
+
+
+def cpu_mul_mat_q4_0(w, M, K, x, nb01=None, nthreads=0):
+    """ggml's CPU q4_0 x f32 mat-vec restated with SIMD (Q8_0 activation, int8 block dots): y [ncols, M]."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, K)
+    nb01 = nb01 if nb01 is not None else K // 32 * 18
+    y = np.empty((x.shape[0], M), np.float32)
+    if _cpu_lib().cpu_ggml_mul_mat_q4_0(np.ascontiguousarray(w, np.uint8).ravel(), nb01, M, K, x.ravel(),
+                                        x.shape[0], y.ravel(), nthreads):
+        raise OracleError("cpu_ggml_mul_mat_q4_0: invalid arguments")
+    return y
+
+
+def cpu_fa_decode(n_head_q, n_head_kv, seq_kv, d, q, k16, v16, scale=0.0, nthreads=0):
+    """Decode attention (one query row per head, every key visible) on the CPU with FP32 accumulation."""
+    scale = scale or 1.0 / np.sqrt(d)
+    o = np.empty(n_head_q * d, np.float32)
+    lse = np.empty(n_head_q, np.float32)
+    if _cpu_lib().cpu_ggml_fa_decode(n_head_q, n_head_kv, seq_kv, d, scale, np.ascontiguousarray(q, np.float32),
+                                     np.ascontiguousarray(k16, np.uint16).ravel(),
+                                     np.ascontiguousarray(v16, np.uint16).ravel(), o, lse, nthreads):
+        raise OracleError("cpu_ggml_fa_decode: invalid arguments")
     return o, lse
 
 

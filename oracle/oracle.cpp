@@ -601,6 +601,29 @@ int orc_mul_mat_vec(int type, const uint8_t* w, int64_t nb01, int64_t M, int64_t
     return 0;
 }
 
+int orc_weight_norms(int type, const uint8_t* w, int64_t nb01, int64_t M, int64_t K, double* out, int nthreads) {
+    if (!known(type)) return fail("unknown weight type");
+    if (K <= 0 || K % bsize(type) || K > INT32_MAX) return fail("whole weight blocks required");
+    if (M <= 0) return fail("M must be positive");
+    if (nb01 < K / bsize(type) * bbytes(type)) return fail("row stride shorter than a row");
+    // The same sum as orc_evaluate_row's weight_norm, in the same order.
+#pragma omp parallel for num_threads(threads_for(nthreads)) schedule(static)
+    for (int64_t m = 0; m < M; ++m) {
+        const uint8_t* row = w + m * nb01;
+        double n2 = 0;
+        for (int64_t b = 0; b < K / bsize(type); ++b)
+            for (int sub = 0; sub < bsize(type) / 32; ++sub) {
+                const Sub s = decode(type, row + size_t(b) * bbytes(type), sub);
+                for (int i = 0; i < 32; ++i) {
+                    const double v = sub_value(s, i);
+                    n2 += v * v;
+                }
+            }
+        out[m] = std::sqrt(n2);
+    }
+    return 0;
+}
+
 int orc_quantize(int type, const float* x, int64_t k, uint8_t* out) {
     if (!known(type)) return fail("unknown weight type");
     if (k <= 0 || k % bsize(type)) return fail("whole weight blocks required");
@@ -848,11 +871,12 @@ int orc_fa_decode_f32(const orc_attn_params* pp, const float* q, const uint16_t*
                       const float* mask, float* o, float* lse, int nthreads) {
     const orc_attn_params& p = *pp;
     if (const char* why = attn_invalid(p)) return fail(why);
-    static std::vector<float> table;
-    if (table.empty()) {
-        table.resize(65536);
-        for (int i = 0; i < 65536; ++i) table[size_t(i)] = half_to_float(uint16_t(i));
-    }
+    // Built once on first use; a function-local static initialiser is thread-safe.
+    static const std::vector<float> table = [] {
+        std::vector<float> t(65536);
+        for (int i = 0; i < 65536; ++i) t[size_t(i)] = half_to_float(uint16_t(i));
+        return t;
+    }();
     const float scale = eff_scale(p);
     const float ninf = -std::numeric_limits<float>::infinity();
     const int nth = threads_for(nthreads);

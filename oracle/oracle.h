@@ -14,8 +14,13 @@
  *   orc_prepare             src/reference/qmv_model.cpp:53-71 (Q8_1 + h16 activation blocks)
  *   orc_evaluate_row        src/reference/qmv_model.cpp:134-185 (+ per-group int32 sums, + q6_K)
  *   orc_mul_mat_vec         the same arithmetic per row over a ggml MUL_MAT (src0 quantized, ne11 = ncols)
+ *   orc_weight_norms        src/reference/qmv_model.cpp:144,182 (weight_norm) over every row of a matrix
  *   orc_attention_reference src/reference/attention_reference.cpp:87-135
  *   orc_attention_tiled     src/reference/attention_tiled_model.cpp:52-227
+ *   orc_fa_decode_f32       ggml-cpu FLASH_ATTN_EXT decode (ggml-cpu/ops.cpp:8940-9035 @ 79e2e74, as shown in
+ *                           third_party/patches/0003-tests-biased-V-flash-attention-cases.patch:32-63) with the
+ *                           FP32 VKQ accumulator of bench/results/cpu-fa-fp16-2026-10-10/README.md:15-25; pinned
+ *                           against orc_attention_reference (tests/test_oracle_attention.py)
  *   orc_quantize_q4_0/q8_0  ggml quantize_row_q4_0_ref / quantize_row_q8_0_ref (llama.cpp @ 79e2e74)
  *   orc_quantize_q4_K/q6_K  documented max-based quantizers (NOT ggml's iterative search)
  *
@@ -77,6 +82,9 @@ int orc_evaluate_row(int type, const uint8_t* w, const float* x, int k, orc_row_
  * group_sums (nullable, mode 0 only): [ncols][M][K/group]. Rows run in parallel over nthreads (<=0: all). */
 int orc_mul_mat_vec(int type, const uint8_t* w, int64_t nb01, int64_t M, int64_t K, const float* x,
                     int64_t ncols, int mode, float* y, int32_t* group_sums, int nthreads);
+
+/* ||deq(w_row)|| in FP64 for every row: orc_evaluate_row's weight_norm over a whole matrix (rows in parallel). */
+int orc_weight_norms(int type, const uint8_t* w, int64_t nb01, int64_t M, int64_t K, double* out, int nthreads);
 
 /* Quantizers (k multiple of the block size). */
 int orc_quantize(int type, const float* x, int64_t k, uint8_t* out);

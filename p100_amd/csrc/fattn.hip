@@ -350,6 +350,12 @@ __global__ __launch_bounds__(kSplitThreads) void k_fa_split(FaArgs a) {
             } else {
                 kvq.to_f32(bf.v[u][0], vf[u], dv[u]);
             }
+            if constexpr (kLast) {  // rows past the visible end may hold NaN / Inf bits: select zeros (p is 0)
+                const bool ok = key0 + t * KPB + u * GPW < j1;
+                dv[u] = ok ? dv[u] : 0.0f;
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) vf[u][d] = ok ? vf[u][d] : 0.0f;
+            }
         }
 #pragma unroll
         for (int hh = 0; hh < NH; ++hh) {

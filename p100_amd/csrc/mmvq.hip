@@ -928,8 +928,8 @@ hipError_t launch_mmvr_cols(const MmvrPlan& p, int B, const uint8_t* w, int64_t 
 template <int TYPE, int B>
 hipError_t launch_b(const uint8_t* w, int64_t nb01, int M, int K, int rw, const int8_t* xq, const float4* xds,
                     const float* x, float* y, int32_t* gs, hipStream_t stream) {
-    if (gs) rw = 1;  // the group-sum export is a check path: one row per wave
-    // The single-launch form quantizes x itself; it serves one column (p1x_mul_mat_vec takes the Q8_1 pass and the
+    // The group-sum export runs the same rows per wave as the plain launch, so a check with sums exercises the
+    // instantiation the shape dispatches. The single-launch form quantizes x itself; it serves one column (p1x_mul_mat_vec takes the Q8_1 pass and the
     // prepared kernels from two columns on).
     if (x && B != 1) return hipErrorInvalidValue;
     const dim3 grid((M + 4 * rw - 1) / (4 * rw));

@@ -271,3 +271,33 @@ def test_validation_reasons(orc, gpu):
         assert str(e.value) == why
     with pytest.raises(P.P1XError):
         P.flash_attn_decode(P.AttnParams(d_qk=32, d_v=32), z, zh, zh)
+
+
+@pytest.mark.parametrize("n", [1, 63, 513, 1000])
+def test_rows_past_device_length_may_hold_nan(orc, gpu, n):
+    """Rows in [kv_len, seq_kv) are not valid (their bits are arbitrary): filling them with fp16 NaN and Inf must
+    not reach O or LSE. n leaves the last batch of a split partly past the visible end."""
+    import p100_amd as P
+    import torch
+
+    cap, hq, hkv, d = 1024, 32, 8, 128
+    rng = np.random.default_rng(n)
+    q = rng.standard_normal(hq * d).astype(np.float32)
+    k16 = rng.standard_normal((hkv, cap, d)).astype(np.float16)
+    v16 = rng.standard_normal((hkv, cap, d)).astype(np.float16)
+    kp, vp = k16.copy(), v16.copy()
+    kp[:, n:, ::2] = np.float16(np.nan)
+    kp[:, n:, 1::2] = np.float16(np.inf)
+    vp[:, n:, ::2] = np.float16(-np.inf)
+    vp[:, n:, 1::2] = np.float16(np.nan)
+    p = P.AttnParams(1, hq, hkv, 1, cap, d, d, 0.0, 0.0, False)
+    kd = to_dev(kp.view(np.int16)).view(torch.float16)
+    vd = to_dev(vp.view(np.int16)).view(torch.float16)
+    o, lse = P.flash_attn_decode(p, to_dev(q), kd, vd, kv_len=to_dev(np.int32([n])))
+    o, lse = o.cpu().numpy(), lse.cpu().numpy()
+    pm = orc.AttnParams(1, hq, hkv, 1, n, d, d, 0.0, 0.0, False)
+    ref, ref_lse = orc.attention_reference(pm, q, k16[:, :n].astype(np.float32), v16[:, :n].astype(np.float32))
+    assert np.isfinite(o).all() and np.isfinite(lse).all()
+    err = np.abs(o.astype(np.float64) - ref)
+    assert not (err > 1e-3 + 2e-3 * np.abs(ref)).any(), err.max()
+    assert (np.abs(lse.astype(np.float64) - ref_lse) <= 1e-3).all()

@@ -28,7 +28,23 @@ def quant(kv_type, x):
     return blocks, deq_rows(t, blocks)
 
 
-def run(orc, kv_type, p, seed=0, mask=None, scale_kv=1.0, strided=False, kv_len=None, check_len=None):
+def poison_rows(blocks, p, first, d):
+    """Rows at positions >= first of every (batch, KV head) get a NaN / Inf fp16 scale in every block and random
+    quants (rows past the visible length are not valid; their bytes are arbitrary)."""
+    rb = blocks.shape[1]
+    b = blocks.reshape(p.batch, p.n_head_kv, p.seq_kv, rb).copy()
+    bb = rb // (d // 32)
+    tail = b[:, :, first:]
+    tail[...] = np.random.default_rng(first).integers(0, 256, tail.shape, dtype=np.uint8)
+    for blk in range(d // 32):
+        bits = np.uint16(0x7E00 if blk % 2 == 0 else 0x7C00)  # NaN, +Inf
+        tail[..., blk * bb] = bits & 255
+        tail[..., blk * bb + 1] = bits >> 8
+    return b.reshape(-1, rb)
+
+
+def run(orc, kv_type, p, seed=0, mask=None, scale_kv=1.0, strided=False, kv_len=None, check_len=None,
+        poison=False):
     rng = np.random.default_rng(seed)
     nq = p.batch * p.n_head_q * p.seq_q * p.d_qk
     rows = p.batch * p.n_head_kv * p.seq_kv
@@ -38,6 +54,8 @@ def run(orc, kv_type, p, seed=0, mask=None, scale_kv=1.0, strided=False, kv_len=
     dp = P.AttnParams(p.batch, p.n_head_q, p.n_head_kv, p.seq_q, p.seq_kv, p.d_qk, p.d_v, p.scale, p.softcap,
                       bool(p.causal))
     strides = None
+    if poison:  # only the first kv_len rows are read as valid; the reference sees the unpoisoned ones
+        kb, vb = poison_rows(kb, p, kv_len, p.d_qk), poison_rows(vb, p, kv_len, p.d_v)
     kdev, vdev = to_dev(kb), to_dev(vb)
     if strided:  # ggml's cache view: rows of all KV heads interleaved per position ([batch][seq_kv][head][row])
         rb = kb.shape[1]
@@ -103,6 +121,14 @@ def test_strided_cache_view_and_device_length(orc, gpu, kv_type):
     for n in (1, 513, 1024):
         run(orc, kv_type, orc.AttnParams(1, 32, 8, 1, 1024, 128, 128, 0.0, 0.0, False), seed=9, kv_len=n,
             check_len=n)
+
+
+@pytest.mark.parametrize("kv_type", KV_TYPES)
+@pytest.mark.parametrize("n", [1, 63, 513, 1000])
+def test_rows_past_device_length_may_hold_nan(orc, gpu, kv_type, n):
+    """NaN / Inf block scales and random quants in the rows past the device-side length never reach O or LSE."""
+    run(orc, kv_type, orc.AttnParams(1, 32, 8, 1, 1024, 128, 128, 0.0, 0.0, False), seed=10 + n, kv_len=n,
+        check_len=n, poison=True)
 
 
 def test_rejects_bad_arguments(gpu):

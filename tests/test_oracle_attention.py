@@ -480,3 +480,56 @@ def test_bit_identical_to_reference_build(orc, ref):
         a = orc.attention_tiled(p, cfg, q, k, v, mask)
         b = ref.attention_tiled(p, cfg, q, k, v, mask)
         assert all((x.view(np.uint32) == y.view(np.uint32)).all() for x, y in zip(a, b)), trial
+
+
+# ------------------------------------------------------------------ CPU decode attention (fa_decode_f32)
+@pytest.mark.parametrize("nthreads", [1, 8])
+def test_fa_decode_f32_matches_reference(orc, nthreads):
+    """The ggml-style CPU decode attention (fp16 K/V, FP32 online softmax per KV chunk, log-sum-exp merge of the
+    chunks) against the FP64 reference within tolerance.h, at the decode shape (32/8 heads, d 128, 8192 keys,
+    causal). One thread keeps a single chunk; eight threads merge eight, so a wrong rescale or merge fails."""
+    p = orc.AttnParams(n_head_q=32, n_head_kv=8, seq_q=1, seq_kv=8192, d_qk=128, d_v=128, causal=True)
+    rng = np.random.default_rng(8192)
+    q = rng.standard_normal(32 * 128).astype(np.float32)
+    k16 = rng.standard_normal(8 * 8192 * 128).astype(np.float16)
+    v16 = rng.standard_normal(8 * 8192 * 128).astype(np.float16)
+    q[:128] *= 8  # one head with peaked logits: the running max moves late and far
+    o, lse = orc.fa_decode_f32(p, q, k16.view(np.uint16), v16.view(np.uint16), nthreads=nthreads)
+    ref, ref_lse = orc.attention_reference(p, q, k16.astype(np.float32), v16.astype(np.float32))
+    assert out_ok(o, ref).all(), np.abs(o - ref).max()
+    assert lse_ok(lse, ref_lse).all()
+    assert np.abs(o - ref).max() / np.abs(ref).max() <= 2e-3
+
+
+def test_fa_decode_f32_masked_rows_and_softcap(orc):
+    """Two query rows over 600 keys with an additive mask that hides every key of row 0 (O = 0, LSE = -inf) and
+    half of row 1, and a logit softcap; chunks merged over 4 threads."""
+    p = orc.AttnParams(n_head_q=4, n_head_kv=2, seq_q=2, seq_kv=600, d_qk=64, d_v=64, softcap=5.0)
+    rng = np.random.default_rng(600)
+    q = rng.standard_normal(4 * 2 * 64).astype(np.float32) * 2
+    k16 = rng.standard_normal(2 * 600 * 64).astype(np.float16)
+    v16 = rng.standard_normal(2 * 600 * 64).astype(np.float16)
+    mask = np.zeros((2, 600), np.float32)
+    mask[0, :] = -np.inf
+    mask[1, ::2] = -np.inf
+    mask[1, 1::4] = -1.5
+    o, lse = orc.fa_decode_f32(p, q, k16.view(np.uint16), v16.view(np.uint16), mask=mask, nthreads=4)
+    ref, ref_lse = orc.attention_reference(p, q, k16.astype(np.float32), v16.astype(np.float32), mask=mask)
+    assert out_ok(o, ref).all()
+    assert lse_ok(lse, ref_lse).all()
+    rows = o.reshape(4, 2, 64)
+    assert (rows[:, 0] == 0).all() and np.isneginf(lse.reshape(4, 2)[:, 0]).all()
+
+
+def test_weight_norms_match_evaluate_row(orc):
+    """weight_norms is evaluate_row's weight_norm for every row, bit for bit, including a padded row stride."""
+    for tname in ("q4_0", "q8_0", "q4_K", "q6_K"):
+        t = orc.TYPES[tname]
+        k = 512
+        r = orc.Rng(77 + t)
+        w = np.stack([r.random_row(t, k) for _ in range(9)])
+        want = np.array([orc.evaluate_row(t, w[i], np.zeros(k, np.float32)).weight_norm for i in range(9)])
+        assert np.array_equal(orc.weight_norms(t, w, 9, k), want), tname
+        pad = np.zeros((9, w.shape[1] + 6), np.uint8)
+        pad[:, :w.shape[1]] = w
+        assert np.array_equal(orc.weight_norms(t, pad, 9, k, nb01=w.shape[1] + 6), want), tname
