@@ -29,6 +29,8 @@
  *                            p100::attention_reference (include/p100/attention.h:48-49)
  *   p1x_flash_attn_decode_kvlen  the same op over a KV-cache view whose valid length is known only on the device
  *                            (llama.cpp pads the view and masks the tail with the KQ mask; here the length is read)
+ *   p1x_flash_attn_decode_noalloc  the same op with its scratch in the library (no counterpart in the reference;
+ *                            for callers that cannot allocate)
  *   p1x_flash_attn_decode_quant  the same op over a q8_0 / q4_0 KV cache, replacing the F16 conversion kernels that
  *                            ggml runs first (third_party/patches/0001, 0002; bench/micro/dequant_nc.cu:1-14)
  * Decode-step glue and driver (the llama-bench decode runs, bench/phase0.sh:124, of the 8B shape modelled in
@@ -149,6 +151,22 @@ int p1x_flash_attn_decode(const p1x_attn_params* p, const float* q, const uint16
 int p1x_flash_attn_decode_kvlen(const p1x_attn_params* p, const float* q, const uint16_t* k, const uint16_t* v,
                                 const p1x_kv_strides* strides, const float* mask, const int32_t* kv_len, float* o,
                                 float* lse, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * p1x_flash_attn_decode / p1x_flash_attn_decode_kvlen (kv_len optional here) with no workspace argument and no
+ * allocation: the split partials live in a device array of the library, 1 MiB per GPU (P1X_FA_NOALLOC_SCRATCH_BYTES),
+ * held until the process ends. No counterpart in the reference: for callers that cannot allocate device memory
+ * (HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The split plan keeps the partials of
+ * every d_qk <= 128 shape within 0.55 MiB, and of most d_qk = 256 shapes within 1 MiB. Shapes whose partials exceed the array
+ * (p1x_flash_attn_decode_workspace(p) > P1X_FA_NOALLOC_SCRATCH_BYTES) return P1X_EUNSUPPORTED without launching.
+ * Every call on one GPU shares that GPU's array and nothing in it needs to start at zero (each call writes every
+ * partial it reads), so calls that overlap on one GPU (different streams, or host threads racing) race: serialize
+ * them on one stream.
+ */
+#define P1X_FA_NOALLOC_SCRATCH_BYTES ((size_t)1 << 20)
+int p1x_flash_attn_decode_noalloc(const p1x_attn_params* p, const float* q, const uint16_t* k, const uint16_t* v,
+                                  const p1x_kv_strides* strides, const float* mask, const int32_t* kv_len, float* o,
+                                  float* lse, void* stream);
 
 /*
  * Decode attention over a quantized KV cache (llama.cpp's -ctk / -ctv q8_0 or q4_0; kv_type P1X_Q8_0 or P1X_Q4_0

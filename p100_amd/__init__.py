@@ -30,13 +30,14 @@ BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}  # 
 GROUP = {Q4_0: 32, Q8_0: 32, Q4_K: 32, Q6_K: 16}  # elements per exported int32 sum
 ACT = {"q8_1": 0, "h16": 1}
 OK, EINVAL, EUNSUPPORTED, EHIP, EWORKSPACE = 0, 1, 2, 3, 4
+FA_NOALLOC_SCRATCH_BYTES = 1 << 20  # P1X_FA_NOALLOC_SCRATCH_BYTES
 EXPORTS = ["p1x_version", "p1x_init", "p1x_last_error", "p1x_quantize_q8_1", "p1x_prepare_h16",
            "p1x_mul_mat_vec_workspace", "p1x_mul_mat_vec", "p1x_mul_mat_vec_q8_1", "p1x_mul_mat_vec_h16",
            "p1x_attn_validate", "p1x_flash_attn_decode_workspace", "p1x_flash_attn_decode",
            "p1x_flash_attn_decode_kvlen", "p1x_round_to_fp16", "p1x_get_rows", "p1x_rms_norm_q8_1", "p1x_rms_norm_mul_mat_vec",
            "p1x_swiglu_q8_1",
            "p1x_rope_kv_append", "p1x_argmax_workspace", "p1x_argmax", "p1x_llama_workspace", "p1x_llama_decode_step",
-           "p1x_flash_attn_decode_quant"]
+           "p1x_flash_attn_decode_quant", "p1x_flash_attn_decode_noalloc"]
 
 
 class P1XError(RuntimeError):
@@ -96,6 +97,8 @@ def load():
                                                   vp, vp, vp, sz, vp]),
         "p1x_flash_attn_decode_quant": (C.c_int, [C.POINTER(AttnParams), C.c_int, vp, vp, vp, C.POINTER(KVStrides),
                                                   vp, vp, vp, vp, vp, sz, vp]),
+        "p1x_flash_attn_decode_noalloc": (C.c_int, [C.POINTER(AttnParams), vp, vp, vp, C.POINTER(KVStrides), vp, vp,
+                                                    vp, vp, vp]),
         "p1x_round_to_fp16": (C.c_int, [vp, vp, i64, vp]),
         "p1x_get_rows": (C.c_int, [C.c_int, vp, i64, i64, i64, vp, vp, vp]),
         "p1x_rms_norm_q8_1": (C.c_int, [vp, vp, vp, i64, C.c_float, vp, vp, vp, vp]),

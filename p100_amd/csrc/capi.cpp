@@ -11,6 +11,8 @@
 
 #include "capi_internal.h"
 
+static_assert(p1x::kFaScratchBytes == P1X_FA_NOALLOC_SCRATCH_BYTES, "the header states the scratch size");
+
 namespace p1x::capi {
 
 thread_local std::string g_error;
@@ -46,6 +48,13 @@ void init_once() {
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
         g_init_status = P1X_EUNSUPPORTED;
         g_init_error = std::string("this library is built for gfx950 only; device 0 is ") + prop.gcnArchName;
+        return;
+    }
+    void* scratch = nullptr;  // the no-allocation attention scratch of this device, looked up once
+    e = p1x::fa_scratch(&scratch);
+    if (e != hipSuccess) {
+        g_init_status = P1X_EHIP;
+        g_init_error = std::string("scratch symbol: ") + hipGetErrorString(e);
     }
 }
 }  // namespace
@@ -309,6 +318,28 @@ int p1x_flash_attn_decode_kvlen(const p1x_attn_params* p, const float* q, const 
     if (int rc = fa_prepare(p, q, k, v, strides, mask, kv_len, o, lse, ws, ws_bytes, a, true)) return rc;
     hipError_t e = p1x::launch_fa_decode(a, p->batch, p->d_qk, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? P1X_OK : hip_fail(e, "flash_attn_decode_kvlen");
+}
+
+int p1x_flash_attn_decode_noalloc(const p1x_attn_params* p, const float* q, const uint16_t* k, const uint16_t* v,
+                                  const p1x_kv_strides* strides, const float* mask, const int32_t* kv_len, float* o,
+                                  float* lse, void* stream) {
+    if (int rc = ensure_init()) return rc;
+    if (kv_len && !aligned(kv_len, 4)) return fail(P1X_EINVAL, "kv_len must be 4-byte aligned");
+    if (int rc = p1x_attn_validate(p)) return rc;
+    const size_t need = fa_workspace(p);
+    if (need > p1x::kFaScratchBytes)
+        return fail(P1X_EUNSUPPORTED, "the split partials need " + std::to_string(need) +
+                                          " bytes, more than the " + std::to_string(p1x::kFaScratchBytes) +
+                                          "-byte scratch of the no-allocation entry point");
+    void* ws = nullptr;
+    if (need) {
+        hipError_t e = p1x::fa_scratch(&ws);
+        if (e != hipSuccess) return hip_fail(e, "scratch symbol");
+    }
+    p1x::FaArgs a;
+    if (int rc = fa_prepare(p, q, k, v, strides, mask, kv_len, o, lse, ws, need, a, true)) return rc;
+    hipError_t e = p1x::launch_fa_decode(a, p->batch, p->d_qk, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? P1X_OK : hip_fail(e, "flash_attn_decode_noalloc");
 }
 
 int p1x_flash_attn_decode_quant(const p1x_attn_params* p, int kv_type, const float* q, const void* k, const void* v,

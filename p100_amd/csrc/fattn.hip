@@ -22,10 +22,16 @@
 // and LSE itself and pass 2 is skipped.
 // (A single launch, where the last work-group to arrive combines, needs an agent-scope release per work-group:
 // each one writes back the XCD's L2, and one per work-group alone costs more than the second launch.)
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
 #include "launch.h"
+
+// Split partials of p1x_flash_attn_decode_noalloc (callers that cannot allocate): one copy per GPU, held until the
+// process ends. Host code never passes `scratch` itself to a kernel (on the host it names a stand-in, not device
+// memory): fa_scratch() looks up each device's address once and the kernels take that pointer.
+static __device__ __align__(256) unsigned char scratch[p1x::kFaScratchBytes];
 
 #ifndef P1X_FA_PF
 #define P1X_FA_PF 2  // K/V batches in flight per wave
@@ -703,6 +709,28 @@ void fa_split_plan(int batch, int hq, int hkv, int seq_q, int seq_kv, int d, int
     chunk = int((seq_kv + want - 1) / want);
     chunk = (chunk + kpb - 1) / kpb * kpb;
     splits = (seq_kv + chunk - 1) / chunk;
+}
+
+// Address of this device's `scratch`, looked up with hipGetSymbolAddress the first time each device asks (with
+// that device current) and kept per device.
+hipError_t fa_scratch(void** out) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static void* addr[kMaxDevices] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        addr[dev] = p;
+    }
+    *out = addr[dev];
+    return hipSuccess;
 }
 
 hipError_t launch_fa_decode(FaArgs a, int batch, int d, hipStream_t stream) {

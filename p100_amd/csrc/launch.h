@@ -86,6 +86,10 @@ struct FaArgs {
     float scale, softcap;
 };
 hipError_t launch_fa_decode(FaArgs a, int batch, int d, hipStream_t stream);
+// Device scratch of the no-allocation attention entry point: a file-scope array of kFaScratchBytes in fattn.hip,
+// whose address on the current device fa_scratch() returns (looked up once per device).
+constexpr size_t kFaScratchBytes = size_t(1) << 20;
+hipError_t fa_scratch(void** out);
 int fa_heads_per_wg(int hq, int hkv);
 void fa_split_plan(int batch, int hq, int hkv, int seq_q, int seq_kv, int d, int& splits, int& chunk);
 
