@@ -41,6 +41,13 @@ def fa_bytes(hq, hkv, ctx, d):
     return 2 * hkv * ctx * d * 2 + 2 * hq * d * 4
 
 
+def rotation(set_bytes, total=544 << 20, cap=256):
+    """Distinct buffer sets to rotate over so that the sets one timed graph touches span > 512 MB (twice the
+    256 MB Infinity Cache): each launch then reads bytes the previous ~512 MB of traffic has evicted. The graph
+    holds max(32, sets) launches so that every set is read."""
+    return max(2, min(cap, -(-total // set_bytes)))
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -93,11 +100,14 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline and roofline only")
-    ap.add_argument("--only", choices=("roofline", "fa", "decode", "cols"), default=None,
+    ap.add_argument("--only", choices=("roofline", "fa", "decode", "cols", "kquant", "read", "mmvh"), default=None,
                     help="run one measurement alone (for profiler runs whose per-kernel averages must not mix "
                          "shapes): 'roofline' = the Q4_0 4096x14336 mat-vec, 'fa' = FA decode at --fa-ctx, "
                          "'decode' = the end-to-end 8B greedy decode, 'cols' = the Q4_0 4096x14336 mat-vec on a "
-                         "prepared Q8_1 activation of --cols columns")
+                         "prepared Q8_1 activation of --cols columns, 'kquant' = the K-quant kernels (--kquant "
+                         "picks one shape), 'read' = the read-ceiling probe, 'mmvh' = the h16 kernels")
+    ap.add_argument("--kquant", default=None, help="with --only kquant: one of q4_K:14336x4096, q4_K:4096x14336, "
+                                                     "q6_K:128256x4096")
     ap.add_argument("--cols", type=int, nargs="+", default=[4, 16])
     ap.add_argument("--fa-ctx", type=int, nargs="+", default=[512, 640, 2048, 8192, 32768])
     ap.add_argument("--fa-fp16-only", action="store_true",
@@ -143,6 +153,18 @@ def main():
             log(f"[bench] Q4_0 {M}x{K} at {n} columns (prepared Q8_1): {med:.2f} us")
         print(json.dumps({"only": "cols", "q4_0_4096x14336_prepared": rec}))
         return
+    if args.only in ("kquant", "read", "mmvh"):
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(99)
+        timer = GraphTimer(torch)
+        if args.only == "read":
+            print(json.dumps({"only": "read", "read_ceiling": measure_read_ceiling(torch, lib, timer)}))
+        elif args.only == "kquant":
+            print(json.dumps({"only": "kquant", "kquant": measure_kquant(torch, P, lib, synth, timer, gen,
+                                                                         args.kquant)}))
+        else:
+            print(json.dumps({"only": "mmvh", "mmvh": measure_mmvh(torch, P, lib, synth, timer, gen)}))
+        return
     log(f"[bench] {torch.cuda.get_device_name(0)}; building {args.layers} Q4_0 layers")
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1234)
@@ -155,7 +177,7 @@ def main():
     timer = GraphTimer(torch)
     torch.cuda.synchronize()
     if args.only == "roofline":
-        roof = measure_roofline(torch, P, lib, timer, layers, xs[14336])
+        roof = measure_roofline(torch, P, lib, timer, gen, xs[14336])
         # Calibration for hardware byte counters: a plain 32 MiB device copy (reads and writes 33,554,432 B).
         src = torch.empty(32 << 20, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
@@ -223,7 +245,7 @@ def main():
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     log(f"[bench] layer step {ms_per_step * 1e3:.2f} us, {value:.1f} GB/s ({steps_done} steps in graphs of {n_graph})")
 
-    roof = measure_roofline(torch, P, lib, timer, layers, xs[14336])
+    roof = measure_roofline(torch, P, lib, timer, gen, xs[14336])
 
     result = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps_done,
@@ -244,21 +266,28 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-def measure_roofline(torch, P, lib, timer, layers, x):
-    """Dominant kernel: the Q4_0 4096x14336 mat-vec on a prepared Q8_1 activation, rotated over the weight sets."""
+def measure_roofline(torch, P, lib, timer, gen, x):
+    """Dominant kernel: the Q4_0 4096x14336 mat-vec on a prepared Q8_1 activation, rotated over 16 weight sets
+    (530 MB)."""
+    from p100_amd import synth
+
+    M, K = 4096, 14336
+    b = matvec_bytes(P.Q4_0, M, K, 1)
+    nsets = rotation(M * K // 32 * 18)
+    wsets = [synth.random_weights(P.Q4_0, M, K, generator=gen) for _ in range(nsets)]
     q81 = P.quantize_q8_1(x)
-    y = torch.empty(4096, device=x.device)
+    y = torch.empty(M, device=x.device)
 
     def down(i, s):
-        w = layers[i % len(layers)]["down"]
-        ok(lib, lib.p1x_mul_mat_vec_q8_1(P.Q4_0, C.c_void_p(w.data_ptr()), 14336 // 32 * 18, 4096, 14336,
+        w = wsets[i % nsets]
+        ok(lib, lib.p1x_mul_mat_vec_q8_1(P.Q4_0, C.c_void_p(w.data_ptr()), K // 32 * 18, M, K,
                                          C.c_void_p(q81.qs.data_ptr()), C.c_void_p(q81.ds.data_ptr()), 1,
                                          C.c_void_p(y.data_ptr()), None, s), "roofline mat-vec")
 
-    med, mn, _ = timer.period_us(down)
-    b = matvec_bytes(P.Q4_0, 4096, 14336, 1)
+    med, mn, _ = timer.period_us(down, n=max(64, nsets))
+    del wsets
     achieved = b / (med * 1e-6) / 1e9
-    log(f"[bench] Q4_0 4096x14336 mat-vec kernel {med:.2f} us (min {mn:.2f}) -> {achieved:.0f} GB/s")
+    log(f"[bench] Q4_0 4096x14336 mat-vec kernel {med:.2f} us (min {mn:.2f}) -> {achieved:.0f} GB/s ({nsets} sets)")
     # HBM bytes per launch of this kernel from the FETCH_SIZE / WRITE_SIZE profiler passes (calibrated against a
     # 32 MiB copy), recorded next to the rocprof summary; null when that record is absent.
     traffic, src = None, None
@@ -272,7 +301,73 @@ def measure_roofline(torch, P, lib, timer, layers, x):
                       "x 4 rows, 2 units per lane)", "bound": "hbm",
             "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4),
             "traffic": traffic, "traffic_unit": "bytes per launch", "traffic_source": src,
-            "algorithmic_bytes": b, "avg_us": round(med, 3), "min_us": round(mn, 3)}
+            "algorithmic_bytes": b, "avg_us": round(med, 3), "min_us": round(mn, 3),
+            "rotation": f"{nsets} weight sets, {nsets * M * K // 32 * 18 / 1e6:.0f} MB"}
+
+
+def measure_read_ceiling(torch, lib, timer, nbytes=33103872 // 16 * 16):
+    """The single-launch read ceiling: p1x_read_bytes over the roofline kernel's byte count, rotated over > 512 MB,
+    for several grid sizes; the fastest is the ceiling any one kernel reading these bytes once can reach."""
+    nsets = rotation(nbytes)
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(i) for i in range(nsets)]
+    digest = torch.empty(65536, dtype=torch.int32, device="cuda")
+    by_grid = {}
+    for wgs in (1024, 2048, 4096, 8192):
+        def call(i, s, wgs=wgs):
+            ok(lib, lib.p1x_read_bytes(C.c_void_p(bufs[i % nsets].data_ptr()), nbytes, C.c_void_p(digest.data_ptr()),
+                                       wgs, s), "read_bytes")
+
+        med, mn, _ = timer.period_us(call, n=max(64, nsets))
+        by_grid[str(wgs)] = {"us": round(med, 3), "gbs": round(nbytes / (med * 1e-6) / 1e9, 1)}
+    del bufs
+    best = min(by_grid, key=lambda k: by_grid[k]["us"])
+    us = by_grid[best]["us"]
+    log(f"[bench] read ceiling {nbytes / 1e6:.1f} MB: {us:.2f} us ({nbytes / (us * 1e-6) / 1e9:.0f} GB/s, "
+        f"{best} work-groups)")
+    return {"bytes": nbytes, "us": us, "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "frac": round(nbytes / (us * 1e-6) / 1e9 / PEAK_GBS, 4), "work_groups": int(best), "by_grid": by_grid,
+            "kernel": "k_read_bytes: non-temporal 16-byte loads, 4 in flight per thread, grid-stride, one launch",
+            "rotation": f"{nsets} buffers, {nsets * nbytes / 1e6:.0f} MB"}
+
+
+def measure_matvec(torch, P, lib, synth, timer, gen, wtype, M, K, ncols, act="q8_1", prepared=True):
+    """Per-launch period of one mat-vec shape over > 512 MB of rotated weights: the prepared-activation kernel
+    alone (prepared=True) or the whole op from an f32 activation (quantize / pre-pass + mat-vec)."""
+    rb = P.row_bytes(wtype, K)
+    nsets = rotation(M * rb)
+    wsets = [synth.random_weights(wtype, M, K, generator=gen) for _ in range(nsets)]
+    x = torch.randn((ncols, K), device="cuda", generator=gen)
+    y = torch.empty((ncols, M), device="cuda")
+    if prepared and act == "q8_1":
+        a = P.quantize_q8_1(x)
+
+        def call(i, s):
+            ok(lib, lib.p1x_mul_mat_vec_q8_1(wtype, C.c_void_p(wsets[i % nsets].data_ptr()), rb, M, K,
+                                             C.c_void_p(a.qs.data_ptr()), C.c_void_p(a.ds.data_ptr()), ncols,
+                                             C.c_void_p(y.data_ptr()), None, s), "mul_mat_vec_q8_1")
+    elif prepared:
+        a = P.prepare_h16(x)
+
+        def call(i, s):
+            ok(lib, lib.p1x_mul_mat_vec_h16(wtype, C.c_void_p(wsets[i % nsets].data_ptr()), rb, M, K,
+                                            C.c_void_p(a.h.data_ptr()), C.c_void_p(a.meta.data_ptr()), ncols,
+                                            C.c_void_p(y.data_ptr()), s), "mul_mat_vec_h16")
+    else:
+        mode = P.ACT[act]
+        wsz = lib.p1x_mul_mat_vec_workspace(wtype, M, K, ncols, mode)
+        wsb = torch.empty(max(wsz, 256), dtype=torch.uint8, device="cuda")
+
+        def call(i, s):
+            ok(lib, lib.p1x_mul_mat_vec(wtype, C.c_void_p(wsets[i % nsets].data_ptr()), rb, M, K, mode,
+                                        C.c_void_p(x.data_ptr()), ncols, C.c_void_p(y.data_ptr()), None,
+                                        C.c_void_p(wsb.data_ptr()), wsb.numel(), s), "mul_mat_vec")
+
+    med, mn, _ = timer.period_us(call, n=max(32, nsets))
+    del wsets
+    b = matvec_bytes(wtype, M, K, ncols)
+    gbs = b / (med * 1e-6) / 1e9
+    return {"us": round(med, 3), "min_us": round(mn, 3), "gbs": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4),
+            "sets": nsets}
 
 
 def measure_fa(torch, P, lib, timer, gen, ctxs, kvlen_runs=True):
@@ -281,7 +376,7 @@ def measure_fa(torch, P, lib, timer, gen, ctxs, kvlen_runs=True):
     fa = {}
     for ctx in ctxs:
         p = P.AttnParams(n_head_q=32, n_head_kv=8, seq_q=1, seq_kv=ctx, d_qk=128, d_v=128, causal=True)
-        nsets = max(2, min(16, (600 << 20) // (2 * 8 * ctx * 128 * 2)))
+        nsets = rotation(2 * 8 * ctx * 128 * 2)
         caches = [(torch.randn(8 * ctx * 128, device=dev, generator=gen).half(),
                    torch.randn(8 * ctx * 128, device=dev, generator=gen).half()) for _ in range(nsets)]
         q = torch.randn(32 * 128, device=dev, generator=gen)
@@ -296,10 +391,11 @@ def measure_fa(torch, P, lib, timer, gen, ctxs, kvlen_runs=True):
                                               C.c_void_p(lse.data_ptr()), C.c_void_p(fws.data_ptr()),
                                               fws.numel() * 4, s), "flash_attn_decode")
 
-        med, mn, _ = timer.period_us(call, n=32)
+        med, mn, _ = timer.period_us(call, n=max(32, nsets))
         b = fa_bytes(32, 8, ctx, 128)
         fa[str(ctx)] = {"us": round(med, 3), "min_us": round(mn, 3), "bytes": b,
-                        "gbs": round(b / (med * 1e-6) / 1e9, 1), "frac": round(b / (med * 1e-6) / 1e9 / PEAK_GBS, 4)}
+                        "gbs": round(b / (med * 1e-6) / 1e9, 1), "frac": round(b / (med * 1e-6) / 1e9 / PEAK_GBS, 4),
+                        "sets": nsets}
         log(f"[bench] FA decode ctx {ctx}: {med:.2f} us ({fa[str(ctx)]['gbs']} GB/s)")
         del caches
     # A short visible length in a large cache (device-side length, plan made for the capacity): the kernels spread
@@ -309,7 +405,7 @@ def measure_fa(torch, P, lib, timer, gen, ctxs, kvlen_runs=True):
         return {"config": "32 q heads / 8 kv heads, d 128, 1 query row, causal, fp16 K/V, fp32 o + lse; split-K "
                           "pass + LSE combine pass (2 launches, timed together)", "by_ctx": fa}
     p = P.AttnParams(n_head_q=32, n_head_kv=8, seq_q=1, seq_kv=cap, d_qk=128, d_v=128, causal=True)
-    nsets = max(2, min(16, (600 << 20) // (2 * 8 * cap * 128 * 2)))
+    nsets = rotation(2 * 8 * cap * 128 * 2)
     caches = [(torch.randn(8 * cap * 128, device=dev, generator=gen).half(),
                torch.randn(8 * cap * 128, device=dev, generator=gen).half()) for _ in range(nsets)]
     q = torch.randn(32 * 128, device=dev, generator=gen)
@@ -328,7 +424,7 @@ def measure_fa(torch, P, lib, timer, gen, ctxs, kvlen_runs=True):
                                                     C.c_void_p(lse.data_ptr()), C.c_void_p(fws.data_ptr()),
                                                     fws.numel() * 4, s), "flash_attn_decode_kvlen")
 
-        med, mn, _ = timer.period_us(call, n=32)
+        med, mn, _ = timer.period_us(call, n=max(32, nsets))
         kvlen[str(n)] = {"us": round(med, 3), "min_us": round(mn, 3)}
         log(f"[bench] FA decode, {n} visible keys in a cache of {cap}: {med:.2f} us")
     del caches
@@ -346,7 +442,7 @@ def measure_fa_quant(torch, P, lib, synth, timer, gen, ctxs, kv_type):
     fa = {}
     for ctx in ctxs:
         p = P.AttnParams(n_head_q=32, n_head_kv=8, seq_q=1, seq_kv=ctx, d_qk=128, d_v=128, causal=True)
-        nsets = max(2, min(16, (600 << 20) // (2 * 8 * ctx * row)))
+        nsets = rotation(2 * 8 * ctx * row)
         caches = [(synth.random_weights(t, 8 * ctx, 128, std=1.0, generator=gen),
                    synth.random_weights(t, 8 * ctx, 128, std=1.0, generator=gen)) for _ in range(nsets)]
         q = torch.randn(32 * 128, device=dev, generator=gen)
@@ -362,13 +458,53 @@ def measure_fa_quant(torch, P, lib, synth, timer, gen, ctxs, kv_type):
                                                     C.c_void_p(fws.data_ptr()), fws.numel() * 4, s),
                "flash_attn_decode_quant")
 
-        med, mn, _ = timer.period_us(call, n=32)
+        med, mn, _ = timer.period_us(call, n=max(32, nsets))
         b = 2 * 8 * ctx * row + 32 * 128 * 4 * 2  # quantized K and V once per KV head, q and o in f32
         fa[str(ctx)] = {"us": round(med, 3), "min_us": round(mn, 3), "bytes": b,
                         "gbs": round(b / (med * 1e-6) / 1e9, 1), "frac": round(b / (med * 1e-6) / 1e9 / PEAK_GBS, 4)}
         log(f"[bench] FA decode {kv_type} KV ctx {ctx}: {med:.2f} us ({fa[str(ctx)]['gbs']} GB/s)")
         del caches
     return {"config": f"as fa_decode with a {kv_type} KV cache dequantized in-kernel", "by_ctx": fa}
+
+
+KQUANT_SHAPES = [("q4_K", 14336, 4096), ("q4_K", 4096, 14336), ("q6_K", 128256, 4096)]
+
+
+def measure_kquant(torch, P, lib, synth, timer, gen, only=None):
+    """The K-quant configuration at ne11 = 1: Q4_K FFN matrices and the Q6_K output projection, as the whole op
+    from an f32 activation (Q8_1 quantize + mat-vec) and as the mat-vec kernel on a prepared activation."""
+    out = {}
+    for tname, M, K in KQUANT_SHAPES:
+        key = f"{tname}:{M}x{K}"
+        if only and key != only:
+            continue
+        t = P.TYPES[tname]
+        kern = measure_matvec(torch, P, lib, synth, timer, gen, t, M, K, 1, prepared=True)
+        op = measure_matvec(torch, P, lib, synth, timer, gen, t, M, K, 1, prepared=False)
+        out[f"{tname} {M}x{K} n=1"] = {"kernel": kern, "op": op}
+        log(f"[bench] {tname} {M}x{K}: kernel {kern['us']} us ({kern['gbs']} GB/s, frac {kern['frac']}), "
+            f"op {op['us']} us")
+    return out
+
+
+MMVH_SHAPES = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]
+
+
+def measure_mmvh(torch, P, lib, synth, timer, gen):
+    """The h16 (MMVH) mat-vec kernel against the Q8_1 (MMVQ) kernel on prepared activations, at the Llama-3-8B
+    layer shapes, ne11 in {1, 4, 8}: the measurements behind p1x_should_use_mmvh."""
+    out = {}
+    for tname in ("q4_0", "q8_0", "q4_K", "q6_K"):
+        t = P.TYPES[tname]
+        for M, K in MMVH_SHAPES:
+            for n in (1, 4, 8):
+                h = measure_matvec(torch, P, lib, synth, timer, gen, t, M, K, n, act="h16", prepared=True)
+                q = measure_matvec(torch, P, lib, synth, timer, gen, t, M, K, n, act="q8_1", prepared=True)
+                out[f"{tname} {M}x{K} n={n}"] = {"h16_us": h["us"], "q8_1_us": q["us"], "h16_gbs": h["gbs"],
+                                                  "q8_1_gbs": q["gbs"]}
+        log(f"[bench] mmvh {tname}: " + ", ".join(f"{k.split(' ', 1)[1]} h16 {v['h16_us']} / q8_1 {v['q8_1_us']} us"
+                                                for k, v in out.items() if k.startswith(tname)))
+    return out
 
 
 def extra_measurements(torch, P, lib, synth, timer, gen, layers, xs, ctxs):
@@ -413,9 +549,9 @@ def extra_measurements(torch, P, lib, synth, timer, gen, layers, xs, ctxs):
     sweep = {}
     for wtype, tname in ((P.Q4_0, "q4_0"), (P.Q8_0, "q8_0")):
         for name, M, K in (("wq", 4096, 4096), ("wk", 1024, 4096), ("gate", 14336, 4096), ("down", 4096, 14336)):
-            nsets = max(2, min(8, (600 << 20) // (M * K)))
-            wsets = [synth.random_weights(wtype, M, K, generator=gen) for _ in range(nsets)]
             rb = P.row_bytes(wtype, K)
+            nsets = rotation(M * rb)
+            wsets = [synth.random_weights(wtype, M, K, generator=gen) for _ in range(nsets)]
             for n in (1, 2, 4, 8, 16):  # 16: the int8 matrix-core form (9..16 columns)
                 x = torch.randn((n, K), device=dev, generator=gen)
                 y = torch.empty((n, M), device=dev)
@@ -427,13 +563,16 @@ def extra_measurements(torch, P, lib, synth, timer, gen, layers, xs, ctxs):
                                                 C.c_void_p(x.data_ptr()), n, C.c_void_p(y.data_ptr()), None,
                                                 C.c_void_p(wsb.data_ptr()), wsz, s), "mul_mat_vec")
 
-                med, _, _ = timer.period_us(call, n=32)
+                med, _, _ = timer.period_us(call, n=max(32, nsets))
                 b = matvec_bytes(wtype, M, K, n)
                 sweep[f"{tname} {M}x{K} n={n}"] = {"us": round(med, 3), "gbs": round(b / (med * 1e-6) / 1e9, 1)}
             del wsets
     out["matvec_sweep_op_us"] = sweep
     log("[bench] sweep n=1: " + ", ".join(f"{k}: {v['us']}us {v['gbs']}" for k, v in sweep.items() if k.endswith("n=1")))
 
+    out["read_ceiling"] = measure_read_ceiling(torch, lib, timer)
+    out["kquant"] = measure_kquant(torch, P, lib, synth, timer, gen)
+    out["mmvh_vs_mmvq"] = measure_mmvh(torch, P, lib, synth, timer, gen)
     out["fa_decode"] = measure_fa(torch, P, lib, timer, gen, sorted(set(ctxs) | {640}))
     fa = out["fa_decode"]["by_ctx"]
     for kv_type in ("q8_0", "q4_0"):
@@ -510,26 +649,54 @@ def measure_decode(torch, n_prompt=512, n_gen=256, seed=7):
     return out
 
 
+def _timed_runs(fn, seconds, min_runs=5):
+    fn()  # warm-up
+    times = []
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds or len(times) < min_runs:
+        a = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - a)
+    times.sort()
+    return times
+
+
 def cpu_baseline(P, w_dev, x_dev, seconds):
-    """The CPU oracle's Q8_1 integer mat-vec (OpenMP over rows) on the same 4096x14336 Q4_0 matrix and input,
-    repeated for about `seconds` seconds on this host; reported in GB/s with the same byte count."""
+    """ggml's CPU path restated with SIMD (oracle/cpu_ggml.cpp: Q8_0 activation and AVX-512 VNNI int8 block dots
+    for the Q4_0 mat-vec; FP32-accumulating decode attention with F16C), timed on this host's cores on the same
+    4096x14336 Q4_0 matrix and input as the roofline kernel, and FA decode at 8192 keys (32/8 heads, d 128); each
+    the median of at least 5 runs over about seconds / 2."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import numpy as np
+
     import oracle
 
+    oracle.build()
     w = w_dev.cpu().numpy()
     x = x_dev.cpu().numpy().reshape(1, -1)
     M, K = 4096, 14336
-    oracle.mul_mat_vec(P.Q4_0, w, M, K, x)  # warm-up
-    times = []
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds or len(times) < 3:
-        a = time.perf_counter()
-        oracle.mul_mat_vec(P.Q4_0, w, M, K, x)
-        times.append(time.perf_counter() - a)
-    times.sort()
-    med = times[len(times) // 2]
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or oracle.max_threads()
+    # 32 copies of the matrix (1.06 GB), one per run in turn, so the host's last-level cache (up to a few hundred MB
+    # on server parts) cannot hold the weights between runs.
+    copies = [w.copy() for _ in range(32)]
+    it = iter(range(1 << 60))
+    mv = _timed_runs(lambda: oracle.cpu_mul_mat_q4_0(copies[next(it) % 32], M, K, x, nthreads=threads), seconds / 2)
+    del copies
+    med = mv[len(mv) // 2]
     b = matvec_bytes(P.Q4_0, M, K, 1)
-    threads = oracle.max_threads()
+    rng = np.random.default_rng(8192)
+    q = rng.standard_normal(32 * 128).astype(np.float32)
+    kv = [(rng.standard_normal(8 * 8192 * 128).astype(np.float16).view(np.uint16),
+           rng.standard_normal(8 * 8192 * 128).astype(np.float16).view(np.uint16)) for _ in range(16)]  # 537 MB
+    it2 = iter(range(1 << 60))
+
+    def fa_run():
+        k16, v16 = kv[next(it2) % 16]
+        oracle.cpu_fa_decode(32, 8, 8192, 128, q, k16, v16, nthreads=threads)
+
+    fa = _timed_runs(fa_run, seconds / 2)
+    del kv
+    fa_med = fa[len(fa) // 2]
     cpu = "unknown"
     try:
         with open("/proc/cpuinfo") as f:
@@ -539,10 +706,17 @@ def cpu_baseline(P, w_dev, x_dev, seconds):
                     break
     except OSError:
         pass
-    log(f"[bench] CPU oracle q4_0 4096x14336: {med * 1e3:.2f} ms median over {len(times)} runs, {threads} threads")
+    isa = "AVX-512 VNNI" if oracle.cpu_uses_vnni() else "AVX2"
+    log(f"[bench] CPU q4_0 4096x14336 ({isa}): {med * 1e3:.3f} ms median of {len(mv)}; FA ctx 8192 "
+        f"{fa_med * 1e6:.0f} us median of {len(fa)}; {threads} threads, {cpu}")
     return {"value": round(b / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"Q4_0 4096x14336 ne11=1 op (Q8_1 quantize + integer dot), {len(times)} runs in "
-                      f"{sum(times):.1f} s, median {med * 1e3:.2f} ms; scalar C++ restatement, OpenMP over rows; {cpu}"}
+            "sample": f"Q4_0 4096x14336 ne11=1 op (Q8_0 quantize of x + int8 block dots, ggml's CPU path restated "
+                      f"with {isa}, OpenMP over rows) over 32 rotated copies of the matrix (1.06 GB): median "
+                      f"{med * 1e3:.3f} ms of {len(mv)} runs (min {mv[0] * 1e3:.3f}, max {mv[-1] * 1e3:.3f}); {cpu}",
+            "fa_decode_ctx8192": {"us": round(fa_med * 1e6, 1), "runs": len(fa),
+                                  "gbs": round(fa_bytes(32, 8, 8192, 128) / fa_med / 1e9, 2),
+                                  "note": "32/8 heads, d 128, fp16 K/V (16 rotated caches, 537 MB), FP32 online "
+                                          "softmax per (head, KV chunk), chunks merged by log-sum-exp; F16C + FMA"}}
 
 
 if __name__ == "__main__":

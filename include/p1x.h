@@ -179,6 +179,12 @@ int p1x_flash_attn_decode_quant(const p1x_attn_params* p, int kv_type, const flo
                                 const p1x_kv_strides* byte_strides, const float* mask, const int32_t* kv_len, float* o,
                                 float* lse, void* ws, size_t ws_bytes, void* stream);
 
+/* Measurement: reads `bytes` (16-byte aligned, a multiple of 16) once with non-temporal loads in one launch of
+ * work_groups x 256 threads and writes an XOR digest per work-group into digest[work_groups]. Its time per launch
+ * is the single-launch HBM read ceiling the mat-vec and attention rooflines are set against (no counterpart in
+ * the reference; the bench reports it as read_ceiling). */
+int p1x_read_bytes(const void* src, size_t bytes, uint32_t* digest, int work_groups, void* stream);
+
 /* fp32 -> IEEE binary16 bits with the device conversion the kernels use (round to nearest even). */
 int p1x_round_to_fp16(const float* x, uint16_t* out, int64_t n, void* stream);
 

@@ -37,7 +37,7 @@ EXPORTS = ["p1x_version", "p1x_init", "p1x_last_error", "p1x_quantize_q8_1", "p1
            "p1x_flash_attn_decode_kvlen", "p1x_round_to_fp16", "p1x_get_rows", "p1x_rms_norm_q8_1", "p1x_rms_norm_mul_mat_vec",
            "p1x_swiglu_q8_1",
            "p1x_rope_kv_append", "p1x_argmax_workspace", "p1x_argmax", "p1x_llama_workspace", "p1x_llama_decode_step",
-           "p1x_flash_attn_decode_quant", "p1x_flash_attn_decode_noalloc"]
+           "p1x_flash_attn_decode_quant", "p1x_flash_attn_decode_noalloc", "p1x_read_bytes"]
 
 
 class P1XError(RuntimeError):
@@ -99,6 +99,7 @@ def load():
                                                   vp, vp, vp, vp, vp, sz, vp]),
         "p1x_flash_attn_decode_noalloc": (C.c_int, [C.POINTER(AttnParams), vp, vp, vp, C.POINTER(KVStrides), vp, vp,
                                                     vp, vp, vp]),
+        "p1x_read_bytes": (C.c_int, [vp, sz, vp, C.c_int, vp]),
         "p1x_round_to_fp16": (C.c_int, [vp, vp, i64, vp]),
         "p1x_get_rows": (C.c_int, [C.c_int, vp, i64, i64, i64, vp, vp, vp]),
         "p1x_rms_norm_q8_1": (C.c_int, [vp, vp, vp, i64, C.c_float, vp, vp, vp, vp]),

@@ -58,7 +58,42 @@ __global__ __launch_bounds__(256) void k_round_fp16(const float* __restrict__ x,
     if (i < n) out[i] = __half_as_ushort(__float2half(x[i]));
 }
 
+// Read ceiling probe: streams n16 16-byte words once with non-temporal loads, 4 loads in flight per thread
+// (grid-stride), and writes one XOR digest per work-group so no load is dead. Its per-launch time is the floor
+// any single kernel that reads the same bytes once can reach.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void k_read_bytes(const u32x4_t* __restrict__ src, int64_t n16,
+                                                    uint32_t* __restrict__ digest) {
+    constexpr int kUnroll = 4;
+    const int64_t stride = int64_t(gridDim.x) * 256;
+    int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    uint32_t acc = 0;
+    for (; i + (kUnroll - 1) * stride < n16; i += kUnroll * stride) {
+        u32x4_t v[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) v[u] = __builtin_nontemporal_load(src + i + u * stride);
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; i < n16; i += stride) {
+        const u32x4_t v = __builtin_nontemporal_load(src + i);
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    __shared__ uint32_t part[4];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc ^= uint32_t(__shfl_xor(int(acc), off));
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) digest[blockIdx.x] = part[0] ^ part[1] ^ part[2] ^ part[3];
+}
+
 }  // namespace
+
+hipError_t launch_read_bytes(const void* src, int64_t bytes, uint32_t* digest, int work_groups, hipStream_t stream) {
+    hipLaunchKernelGGL(k_read_bytes, dim3(work_groups), dim3(256), 0, stream, static_cast<const u32x4_t*>(src),
+                       bytes / 16, digest);
+    return hipGetLastError();
+}
 
 hipError_t launch_quantize_q8_1(const float* x, int8_t* qs, float* ds, int K, int ncols, hipStream_t stream) {
     const dim3 grid((K + 2047) / 2048, ncols);

@@ -395,4 +395,13 @@ int p1x_round_to_fp16(const float* x, uint16_t* out, int64_t n, void* stream) {
     return e == hipSuccess ? P1X_OK : hip_fail(e, "round_to_fp16");
 }
 
+int p1x_read_bytes(const void* src, size_t bytes, uint32_t* digest, int work_groups, void* stream) {
+    if (int rc = ensure_init()) return rc;
+    if (!src || !digest) return fail(P1X_EINVAL, "null pointer");
+    if (bytes == 0 || bytes % 16 || !aligned(src, 16)) return fail(P1X_EINVAL, "src and bytes must be 16-byte multiples");
+    if (work_groups < 1 || work_groups > 65536) return fail(P1X_EINVAL, "work_groups must be 1..65536");
+    hipError_t e = p1x::launch_read_bytes(src, int64_t(bytes), digest, work_groups, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? P1X_OK : hip_fail(e, "read_bytes");
+}
+
 }  // extern "C"

@@ -9,6 +9,7 @@ namespace p1x {
 hipError_t launch_quantize_q8_1(const float* x, int8_t* qs, float* ds, int K, int ncols, hipStream_t stream);
 hipError_t launch_prepare_h16(const float* x, uint16_t* h, float* meta, int K, int ncols, hipStream_t stream);
 hipError_t launch_round_fp16(const float* x, uint16_t* out, int64_t n, hipStream_t stream);
+hipError_t launch_read_bytes(const void* src, int64_t bytes, uint32_t* digest, int work_groups, hipStream_t stream);
 // x != nullptr: the single-launch form (x f32 [K], one column, quantized in-kernel; xq/xds unused; B > 1 is
 // rejected). Else xq/xds hold a prepared Q8_1 activation.
 hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
