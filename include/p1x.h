@@ -14,14 +14,19 @@
  *   - Work-group geometry, tile sizes and split counts are chosen inside the library.
  *
  * Reference interfaces each entry point replaces (paths in the reference repo):
- *   p1x_quantize_q8_1        ggml-cuda quantize_row_q8_1_cuda (mmvq.cu:1536 call site; arithmetic restated
- *                            in src/reference/qmv_model.cpp:53-71, `prepare` q fields)
+ *   p1x_quantize_q8_1        the src1 quantization inside ggml_cuda_mul_mat_vec_q (quantize_row_q8_1_cuda,
+ *                            mmvq.cu:1536; arithmetic src/reference/qmv_model.cpp:53-71) into this library's
+ *                            staging layout (not ggml's block_q8_1; see below)
  *   p1x_prepare_h16          mmvh_h16_prepass (third_party/patches/0005-...-mmvh.patch:185-207),
  *                            bench/micro/h2_mmv.cu:99-113
  *   p1x_mul_mat_vec          ggml_cuda_mul_mat_vec_q (0005 patch hook :402-410) with the MMVH branch
  *                            ggml_cuda_should_use_mmvh / ggml_cuda_mul_mat_vec_h (0005 patch :344-377)
- *   p1x_mul_mat_vec_q8_1     mul_mat_vec_q with an already quantized src1 (mmvq.cu:318); 9..16 columns take the
- *                            place of ggml's mul_mat_q for small batches (docs/research/volta-fa-p9-lessons-2026-10-11.md:23-42)
+ *   p1x_mul_mat_vec_q8_1     the mat-vec stage of ggml_cuda_mul_mat_vec_q (the mul_mat_vec_q launch, mmvq.cu:318) on
+ *                            a src1 staged by p1x_quantize_q8_1; 9..16 columns take the place of ggml's mul_mat_q
+ *                            for small batches (docs/research/volta-fa-p9-lessons-2026-10-11.md:23-42)
+ *   p1x_should_use_mmvh      ggml_cuda_should_use_mmvh (0005 patch :344-352)
+ *   p1x_mul_mat_vec_batched  ggml_cuda_mul_mat_vec_q / mmvh_launch with ne02/ne03 broadcasting over (rows, ne12, ne13)
+ *                            grids (0005 patch :271-275, :287-292, :309-321)
  *   p1x_mul_mat_vec_h16      mmvh_mat_vec launch (0005 patch :277-340, 0006 patch :110-206)
  *   p1x_attn_validate        p100::validate (include/p100/attention.h:43, src/reference/attention_reference.cpp:18-32)
  *   p1x_flash_attn_decode    ggml_cuda_flash_attn_ext for n_q small with f16 K/V (fattn.cu:541-719 selection;
@@ -61,8 +66,9 @@ enum { P1X_OK = 0, P1X_EINVAL = 1, P1X_EUNSUPPORTED = 2, P1X_EHIP = 3, P1X_EWORK
 /* src0 weight types: the ggml_type ids. */
 enum { P1X_Q4_0 = 2, P1X_Q8_0 = 8, P1X_Q4_K = 12, P1X_Q6_K = 14 };
 
-/* Activation modes of the mat-vec: Q8_1 integer dot products (upstream MMVQ) or block-scaled FP16 (MMVH). */
-enum { P1X_ACT_Q8_1 = 0, P1X_ACT_H16 = 1 };
+/* Activation modes of the mat-vec: Q8_1 integer dot products (upstream MMVQ), block-scaled FP16 (MMVH), or AUTO:
+ * the one p1x_should_use_mmvh picks for the shape (the Q8_1 path when group sums are requested). */
+enum { P1X_ACT_Q8_1 = 0, P1X_ACT_H16 = 1, P1X_ACT_AUTO = 2 };
 
 /* Library version (major * 10000 + minor * 100 + patch). */
 int p1x_version(void);
@@ -74,7 +80,22 @@ int p1x_init(void);
 const char* p1x_last_error(void);
 
 /*
- * Q8_1 activation, this library's layout (structure of arrays, per column c of ncols, K % 32 == 0):
+ * Kernel selection for P1X_ACT_AUTO, the counterpart of ggml_cuda_should_use_mmvh (third_party/patches/
+ * 0005-CUDA-half2-mat-vec-for-sm_60-mmvh.patch:344-352): 1 when the h16 (MMVH) path is to be used for src0 of type
+ * wtype, M x K, and ncols (ne11) columns of a contiguous f32 src1, else 0 (the Q8_1 path). The reference prefers
+ * MMVH on sm_60 only; on gfx950 the measured preference is q4_K rows longer than 8192 at 4..8 columns. As in the
+ * reference, the environment is read once: P1X_FORCE_MMVH (any value) selects h16 for every supported shape
+ * (ncols 1..8), and otherwise P1X_DISABLE_MMVH turns the preference off.
+ */
+int p1x_should_use_mmvh(int wtype, int64_t M, int64_t K, int64_t ncols);
+
+/*
+ * Q8_1 activation in this library's own staging layout (structure of arrays, per column c of ncols, K % 32 == 0).
+ * It is the intermediate between ggml-cuda's quantize_row_q8_1_cuda and mul_mat_vec_q (mmvq.cu:1536, :318), which
+ * ggml keeps private to ggml_cuda_mul_mat_vec_q (its block_q8_1 is 36 bytes: half2 {d, s} + 32 int8,
+ * src/reference/qmv_model.cpp:60). The drop-in for that op is p1x_mul_mat_vec, which takes f32 src1 as ggml's hook
+ * receives it; these prepared-activation entry points are this library's own split of it, with the same
+ * arithmetic (d, q and s bit-identical to block_q8_1's values) but its own storage:
  *   qs[c*K + i]          int8   q = round(x / d) (IEEE division, ties away from zero)
  *   ds[(c*K/32 + b)*4]   float4 { d, s, isum, 0 }: d = fp16(amax/127), s = fp16(xor-butterfly sum of x),
  *                               isum = sum of the 32 q values (exact), all stored as float
@@ -102,6 +123,26 @@ int p1x_prepare_h16(const float* x, uint16_t* h, float* meta, int64_t K, int64_t
 size_t p1x_mul_mat_vec_workspace(int wtype, int64_t M, int64_t K, int64_t ncols, int act_mode);
 int p1x_mul_mat_vec(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K, int act_mode, const float* x,
                     int64_t ncols, float* y, int32_t* group_sums, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * GGML_OP_MUL_MAT with ggml's broadcasting over dims 2 and 3: src0 holds ne02 x ne03 matrices of M rows (row stride
+ * nb01, matrix strides nb02 / nb03 bytes), src1 x is contiguous f32 [ne13][ne12][ncols][K], and slice (i2, i3)
+ * multiplies matrix (i2 / (ne12 / ne02), i3 / (ne13 / ne03)) with its ncols columns into dst, element
+ * (i3 * nb3_dst + i2 * nb2_dst + c * nb1_dst) / 4 + m (dst nb0 = 4). ne12 % ne02 == ne13 % ne03 == 0, ne12 and
+ * ne13 <= 65535, ncols * ne12 * ne13 <= 65535, ncols 1..8. act_mode as p1x_mul_mat_vec; ws >=
+ * p1x_mul_mat_vec_batched_workspace(...) bytes, 256-byte aligned. Two launches (the activation pass over all
+ * columns, then one mat-vec launch with a (rows, ne12, ne13) grid); no group sums.
+ */
+typedef struct {
+    int64_t ne02, ne03, nb02, nb03;   /* src0 matrices along dims 2 / 3 and their byte strides */
+    int64_t ne12, ne13;               /* src1 / dst extent along dims 2 / 3 */
+    int64_t nb1_dst, nb2_dst, nb3_dst; /* dst byte strides (column, dim 2, dim 3) */
+} p1x_mm_batch;
+size_t p1x_mul_mat_vec_batched_workspace(int wtype, int64_t M, int64_t K, int64_t ncols, const p1x_mm_batch* b,
+                                         int act_mode);
+int p1x_mul_mat_vec_batched(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K, const p1x_mm_batch* b,
+                            int act_mode, const float* x, int64_t ncols, float* y, void* ws, size_t ws_bytes,
+                            void* stream);
 
 /* The same product from an activation already prepared by p1x_quantize_q8_1 / p1x_prepare_h16, so one
  * preparation can serve several weight matrices (q/k/v, gate/up). */

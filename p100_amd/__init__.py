@@ -28,7 +28,7 @@ TYPES = {"q4_0": Q4_0, "q8_0": Q8_0, "q4_K": Q4_K, "q6_K": Q6_K}
 TYPE_NAMES = {v: k for k, v in TYPES.items()}
 BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}  # (elements, bytes)
 GROUP = {Q4_0: 32, Q8_0: 32, Q4_K: 32, Q6_K: 16}  # elements per exported int32 sum
-ACT = {"q8_1": 0, "h16": 1}
+ACT = {"q8_1": 0, "h16": 1, "auto": 2}
 OK, EINVAL, EUNSUPPORTED, EHIP, EWORKSPACE = 0, 1, 2, 3, 4
 FA_NOALLOC_SCRATCH_BYTES = 1 << 20  # P1X_FA_NOALLOC_SCRATCH_BYTES
 EXPORTS = ["p1x_version", "p1x_init", "p1x_last_error", "p1x_quantize_q8_1", "p1x_prepare_h16",
@@ -37,7 +37,8 @@ EXPORTS = ["p1x_version", "p1x_init", "p1x_last_error", "p1x_quantize_q8_1", "p1
            "p1x_flash_attn_decode_kvlen", "p1x_round_to_fp16", "p1x_get_rows", "p1x_rms_norm_q8_1", "p1x_rms_norm_mul_mat_vec",
            "p1x_swiglu_q8_1",
            "p1x_rope_kv_append", "p1x_argmax_workspace", "p1x_argmax", "p1x_llama_workspace", "p1x_llama_decode_step",
-           "p1x_flash_attn_decode_quant", "p1x_flash_attn_decode_noalloc", "p1x_read_bytes"]
+           "p1x_flash_attn_decode_quant", "p1x_flash_attn_decode_noalloc", "p1x_read_bytes",
+           "p1x_should_use_mmvh", "p1x_mul_mat_vec_batched_workspace", "p1x_mul_mat_vec_batched"]
 
 
 class P1XError(RuntimeError):
@@ -59,6 +60,13 @@ class AttnParams(C.Structure):
 
     def effective_scale(self) -> float:
         return 1.0 / math.sqrt(self.d_qk) if self.scale == 0.0 else self.scale
+
+
+class MMBatch(C.Structure):
+    """p1x_mm_batch: ggml broadcasting of a batched mat-vec over dims 2 and 3."""
+
+    _fields_ = [(n, C.c_int64) for n in ("ne02", "ne03", "nb02", "nb03", "ne12", "ne13", "nb1_dst", "nb2_dst",
+                                         "nb3_dst")]
 
 
 class KVStrides(C.Structure):
@@ -88,6 +96,10 @@ def load():
         "p1x_mul_mat_vec_workspace": (sz, [C.c_int, i64, i64, i64, C.c_int]),
         "p1x_mul_mat_vec": (C.c_int, [C.c_int, vp, i64, i64, i64, C.c_int, vp, i64, vp, vp, vp, sz, vp]),
         "p1x_mul_mat_vec_q8_1": (C.c_int, [C.c_int, vp, i64, i64, i64, vp, vp, i64, vp, vp, vp]),
+        "p1x_should_use_mmvh": (C.c_int, [C.c_int, i64, i64, i64]),
+        "p1x_mul_mat_vec_batched_workspace": (sz, [C.c_int, i64, i64, i64, C.POINTER(MMBatch), C.c_int]),
+        "p1x_mul_mat_vec_batched": (C.c_int, [C.c_int, vp, i64, i64, i64, C.POINTER(MMBatch), C.c_int, vp, i64, vp, vp,
+                                              sz, vp]),
         "p1x_mul_mat_vec_h16": (C.c_int, [C.c_int, vp, i64, i64, i64, vp, vp, i64, vp, vp]),
         "p1x_attn_validate": (C.c_int, [C.POINTER(AttnParams)]),
         "p1x_flash_attn_decode_workspace": (sz, [C.POINTER(AttnParams)]),
@@ -242,6 +254,33 @@ def mul_mat_vec(wtype, w, M, K, x, act="q8_1", nb01=None, group_sums=False, out=
         _check(lib.p1x_mul_mat_vec(wtype, _ptr(w), nb01, M, K, mode, _ptr(x), ncols, _ptr(y), _ptr(gs), _ptr(ws),
                                    ws.numel(), s))
     return (y, gs) if group_sums else y
+
+
+def should_use_mmvh(wtype, M, K, ncols) -> bool:
+    """ggml_cuda_should_use_mmvh's counterpart: the activation path act="auto" takes for this shape."""
+    return bool(load().p1x_should_use_mmvh(TYPES.get(wtype, wtype), M, K, ncols))
+
+
+def mul_mat_vec_batched(wtype, w, M, K, x, ne02=1, ne03=1, nb02=0, nb03=0, act="q8_1", nb01=None, out=None,
+                        stream=None):
+    """GGML_OP_MUL_MAT with broadcasting: w holds ne02 x ne03 matrices (byte strides nb02 / nb03), x is float32
+    [ne13, ne12, ncols, K]; returns y [ne13, ne12, ncols, M] (or writes `out`, same layout)."""
+    import torch
+
+    lib = load()
+    wtype = TYPES.get(wtype, wtype)
+    if nb01 is None:
+        nb01 = row_bytes(wtype, K) if wtype in BLOCK else 0
+    x = x.contiguous()
+    ne13, ne12, ncols = x.shape[0], x.shape[1], x.shape[2]
+    y = out if out is not None else torch.empty((ne13, ne12, ncols, M), dtype=torch.float32, device=w.device)
+    b = MMBatch(ne02, ne03, nb02, nb03, ne12, ne13, y.stride(2) * 4, y.stride(1) * 4, y.stride(0) * 4)
+    mode = ACT[act]
+    need = lib.p1x_mul_mat_vec_batched_workspace(wtype, M, K, ncols, C.byref(b), mode)
+    ws = torch.empty(max(need, 256), dtype=torch.uint8, device=w.device)
+    _check(lib.p1x_mul_mat_vec_batched(wtype, _ptr(w), nb01, M, K, C.byref(b), mode, _ptr(x), ncols, _ptr(y),
+                                       _ptr(ws), ws.numel(), _stream(stream)))
+    return y
 
 
 def mul_mat_vec_workspace(wtype, M, K, ncols, act="q8_1") -> int:

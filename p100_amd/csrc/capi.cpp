@@ -5,6 +5,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -208,8 +209,26 @@ int p1x_prepare_h16(const float* x, uint16_t* h, float* meta, int64_t K, int64_t
     return e == hipSuccess ? P1X_OK : hip_fail(e, "prepare_h16");
 }
 
+int p1x_should_use_mmvh(int wtype, int64_t M, int64_t K, int64_t ncols) {
+    // Read once, as ggml reads GGML_CUDA_FORCE_MMVH / GGML_CUDA_DISABLE_MMVH (0005 patch :346-347).
+    static const bool force = std::getenv("P1X_FORCE_MMVH") != nullptr;
+    static const bool disable = std::getenv("P1X_DISABLE_MMVH") != nullptr;
+    if (block_bytes(wtype) == 0 || M <= 0 || K <= 0 || ncols < 1 || ncols > 8) return 0;
+    // Where the h16 path is the faster one on gfx950 (bench.py mmvh_vs_mmvq at the Llama-3-8B shapes): q4_K rows
+    // longer than 8192 elements at 4..8 columns (4096x14336: 36.3 / 64.8 us against 44.3 / 85.2 us for Q8_1). At
+    // every other measured shape and type the Q8_1 integer path is faster (by 1.2x to 3.8x).
+    const bool preferred = wtype == P1X_Q4_K && K > 8192 && ncols >= 4;
+    return force || (preferred && !disable) ? 1 : 0;
+}
+
+static int resolve_act(int wtype, int64_t M, int64_t K, int64_t ncols, int act_mode) {
+    return act_mode == P1X_ACT_AUTO ? (p1x_should_use_mmvh(wtype, M, K, ncols) ? P1X_ACT_H16 : P1X_ACT_Q8_1)
+                                    : act_mode;
+}
+
 size_t p1x_mul_mat_vec_workspace(int wtype, int64_t M, int64_t K, int64_t ncols, int act_mode) {
     if (K <= 0 || ncols <= 0 || M <= 0) return 0;
+    act_mode = resolve_act(wtype, M, K, ncols, act_mode);
     if (act_mode == P1X_ACT_H16) return h16_bytes(K, ncols);
     // One launch (each work-group quantizes x itself) for one column where that fits (mmvq_fused_fits); from two
     // columns the Q8_1 pass plus the register-resident kernel is as fast or faster (1024x4096 at 2 columns
@@ -250,10 +269,13 @@ int p1x_mul_mat_vec(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K
                     int64_t ncols, float* y, int32_t* group_sums, void* ws, size_t ws_bytes, void* stream) {
     if (int rc = ensure_init()) return rc;
     if (int rc = check_matvec(wtype, w, nb01, M, K, ncols, y,
-                              act_mode == P1X_ACT_Q8_1 && p1x::mmq_supported(wtype, 16) ? 16 : 8))
+                              act_mode != P1X_ACT_H16 && p1x::mmq_supported(wtype, 16) ? 16 : 8))
         return rc;
     if (!x) return fail(P1X_EINVAL, "null activation pointer");
-    if (act_mode != P1X_ACT_Q8_1 && act_mode != P1X_ACT_H16) return fail(P1X_EINVAL, "unknown activation mode");
+    if (act_mode != P1X_ACT_Q8_1 && act_mode != P1X_ACT_H16 && act_mode != P1X_ACT_AUTO)
+        return fail(P1X_EINVAL, "unknown activation mode");
+    if (act_mode == P1X_ACT_AUTO && group_sums) act_mode = P1X_ACT_Q8_1;  // sums exist only on the Q8_1 path
+    act_mode = resolve_act(wtype, M, K, ncols, act_mode);
     if (act_mode == P1X_ACT_H16 && group_sums)
         return fail(P1X_EINVAL, "group sums exist only for the Q8_1 activation mode");
     const size_t need = p1x_mul_mat_vec_workspace(wtype, M, K, ncols, act_mode);
@@ -286,6 +308,65 @@ int p1x_mul_mat_vec(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K
     if (e != hipSuccess) return hip_fail(e, "prepare_h16");
     e = p1x::launch_mmvh(wtype, int(ncols), w, nb01, int(M), int(K), h, meta, y, s);
     return e == hipSuccess ? P1X_OK : hip_fail(e, "mul_mat_vec_h16");
+}
+
+size_t p1x_mul_mat_vec_batched_workspace(int wtype, int64_t M, int64_t K, int64_t ncols, const p1x_mm_batch* b,
+                                         int act_mode) {
+    if (!b || K <= 0 || ncols <= 0 || M <= 0 || b->ne12 <= 0 || b->ne13 <= 0) return 0;
+    const int64_t cols = ncols * b->ne12 * b->ne13;
+    act_mode = resolve_act(wtype, M, K, ncols, act_mode);
+    return act_mode == P1X_ACT_H16 ? h16_bytes(K, cols) : q8_1_bytes(K, cols);
+}
+
+int p1x_mul_mat_vec_batched(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K, const p1x_mm_batch* b,
+                            int act_mode, const float* x, int64_t ncols, float* y, void* ws, size_t ws_bytes,
+                            void* stream) {
+    if (int rc = ensure_init()) return rc;
+    if (!b) return fail(P1X_EINVAL, "null batch description");
+    if (int rc = check_matvec(wtype, w, nb01, M, K, ncols, y, 8)) return rc;
+    if (!x) return fail(P1X_EINVAL, "null activation pointer");
+    if (act_mode != P1X_ACT_Q8_1 && act_mode != P1X_ACT_H16 && act_mode != P1X_ACT_AUTO)
+        return fail(P1X_EINVAL, "unknown activation mode");
+    if (b->ne02 <= 0 || b->ne03 <= 0 || b->ne12 <= 0 || b->ne13 <= 0)
+        return fail(P1X_EINVAL, "ne02, ne03, ne12 and ne13 must be positive");
+    if (b->ne12 % b->ne02 || b->ne13 % b->ne03)
+        return fail(P1X_EINVAL, "ne12 and ne13 must be multiples of ne02 and ne03 (ggml broadcasting)");
+    if (b->ne12 > 65535 || b->ne13 > 65535) return fail(P1X_EINVAL, "ne12 and ne13 must be <= 65535");
+    if (ncols * b->ne12 * b->ne13 > 65535)
+        return fail(P1X_EUNSUPPORTED, "ne11 * ne12 * ne13 activation columns must be <= 65535");
+    if ((b->ne02 > 1 && b->nb02 <= 0) || (b->ne03 > 1 && b->nb03 <= 0) || b->nb02 % 2 || b->nb03 % 2 ||
+        (wtype == P1X_Q4_K && (b->nb02 % 4 || b->nb03 % 4)))
+        return fail(P1X_EINVAL, "weight strides nb02 / nb03 must be positive and keep the rows aligned");
+    const int64_t ycol = b->nb1_dst / 4, y2 = b->nb2_dst / 4, y3 = b->nb3_dst / 4;
+    if (b->nb1_dst % 4 || b->nb2_dst % 4 || b->nb3_dst % 4 || ycol < M || (b->ne12 > 1 && y2 < ycol * ncols) ||
+        (b->ne13 > 1 && y3 < y2 * b->ne12))
+        return fail(P1X_EINVAL, "dst strides nb1 / nb2 / nb3 must be float multiples covering each slice");
+    act_mode = resolve_act(wtype, M, K, ncols, act_mode);
+    const int64_t cols = ncols * b->ne12 * b->ne13;
+    const size_t need = act_mode == P1X_ACT_H16 ? h16_bytes(K, cols) : q8_1_bytes(K, cols);
+    if (!ws || ws_bytes < need) return fail(P1X_EWORKSPACE, "workspace of " + std::to_string(need) + " bytes required");
+    if (!aligned(ws, 256)) return fail(P1X_EINVAL, "workspace must be 256-byte aligned");
+    p1x::Slices sl;
+    sl.w2 = b->nb02, sl.w3 = b->nb03;
+    sl.r2 = int(b->ne12 / b->ne02), sl.r3 = int(b->ne13 / b->ne03);
+    sl.ne12 = int(b->ne12), sl.ne13 = int(b->ne13);
+    sl.ycol = ycol, sl.y2 = y2, sl.y3 = y3;
+    auto* base = static_cast<uint8_t*>(ws);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (act_mode == P1X_ACT_Q8_1) {
+        auto* qs = reinterpret_cast<int8_t*>(base);
+        auto* ds = reinterpret_cast<float*>(base + align256(size_t(K) * cols));
+        hipError_t e = p1x::launch_quantize_q8_1(x, qs, ds, int(K), int(cols), s);
+        if (e != hipSuccess) return hip_fail(e, "quantize_q8_1");
+        e = p1x::launch_mmvq_batched(wtype, int(ncols), w, nb01, int(M), int(K), qs, ds, y, sl, s);
+        return e == hipSuccess ? P1X_OK : hip_fail(e, "mul_mat_vec_batched");
+    }
+    auto* h = reinterpret_cast<uint16_t*>(base);
+    auto* meta = reinterpret_cast<float*>(base + align256(size_t(K) * cols * 2));
+    hipError_t e = p1x::launch_prepare_h16(x, h, meta, int(K), int(cols), s);
+    if (e != hipSuccess) return hip_fail(e, "prepare_h16");
+    e = p1x::launch_mmvh(wtype, int(ncols), w, nb01, int(M), int(K), h, meta, y, s, sl);
+    return e == hipSuccess ? P1X_OK : hip_fail(e, "mul_mat_vec_batched_h16");
 }
 
 int p1x_attn_validate(const p1x_attn_params* p) {

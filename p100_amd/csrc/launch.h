@@ -6,6 +6,17 @@
 
 namespace p1x {
 
+// ggml broadcasting of a batched mat-vec over dims 2 and 3 (GGML_OP_MUL_MAT with ne02 / ne03 > 1 or ne12 / ne13 > 1):
+// grid y = i2 < ne12 and grid z = i3 < ne13; slice (i2, i3) multiplies weight matrix (i2 / r2, i3 / r3), at byte
+// offset (i2 / r2) * w2 + (i3 / r3) * w3, with activation columns (i3 * ne12 + i2) * ncols + c, and writes dst
+// element i2 * y2 + i3 * y3 + c * ycol + row. The defaults are a single slice with dst columns M apart (ycol 0).
+struct Slices {
+    int64_t w2 = 0, w3 = 0;
+    int r2 = 1, r3 = 1;
+    int ne12 = 1, ne13 = 1;
+    int64_t ycol = 0, y2 = 0, y3 = 0;
+};
+
 hipError_t launch_quantize_q8_1(const float* x, int8_t* qs, float* ds, int K, int ncols, hipStream_t stream);
 hipError_t launch_prepare_h16(const float* x, uint16_t* h, float* meta, int K, int ncols, hipStream_t stream);
 hipError_t launch_round_fp16(const float* x, uint16_t* out, int64_t n, hipStream_t stream);
@@ -15,6 +26,10 @@ hipError_t launch_read_bytes(const void* src, int64_t bytes, uint32_t* digest, i
 hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
                        const float* x, float* y, int32_t* gs, hipStream_t stream);
 bool mmvq_fused_fits(int B, int M, int K);
+// The batched (ggml broadcast) mat-vec on a prepared Q8_1 activation of B * ne12 * ne13 columns: the streaming kernel
+// with one slice per grid (y, z) position.
+hipError_t launch_mmvq_batched(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq,
+                               const float* xds, float* y, const Slices& sl, hipStream_t stream);
 // One token's q/k/v projection (one column, prepared Q8_1) with llama.cpp normal-mode RoPE and the KV-cache append
 // done by the mat-vec itself: rows [0, E) of the stacked q/k/v weights are q (rotated into q_out), [E, E+kv) k
 // (rotated, fp16 into k_cache [n_head_kv][n_ctx][d] at *pos), [E+kv, E+2kv) v (fp16 into v_cache); a launch covers
@@ -64,7 +79,7 @@ bool mmq_fits(int M, int64_t nb01, int K, int B);  // weight and activation byte
 hipError_t launch_mmq(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
                       float* y, int32_t* gs, hipStream_t stream);
 hipError_t launch_mmvh(int type, int B, const void* w, int64_t nb01, int M, int K, const uint16_t* h,
-                       const float* meta, float* y, hipStream_t stream);
+                       const float* meta, float* y, hipStream_t stream, const Slices& sl = Slices{});
 
 // Pass-1 arguments of the split-K decode attention (fattn.hip).
 struct FaArgs {

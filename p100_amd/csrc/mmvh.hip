@@ -129,7 +129,16 @@ __device__ __forceinline__ Unpacked unpack(const uint8_t* row, int u) {
 template <int TYPE, int B>
 __global__ __launch_bounds__(256) void k_mmvh(const uint8_t* __restrict__ w, int64_t nb01, int M, int K, int tlog2,
                                               const __half2* __restrict__ h, const float2* __restrict__ meta,
-                                              float* __restrict__ y) {
+                                              float* __restrict__ y, const Slices sl) {
+    if (gridDim.y * gridDim.z > 1) {  // a batched launch: this work-group's slice (ggml broadcasting)
+        const int i2 = blockIdx.y, i3 = blockIdx.z;
+        w += (i2 / sl.r2) * sl.w2 + (i3 / sl.r3) * sl.w3;
+        const int64_t col0 = (int64_t(i3) * sl.ne12 + i2) * B;
+        h += col0 * (K / 2);
+        meta += col0 * (K / 32);
+        y += i2 * sl.y2 + i3 * sl.y3;
+    }
+    const int64_t ycol = sl.ycol ? sl.ycol : M;
     const int T = 1 << tlog2;
     const int t = threadIdx.x & (T - 1);
     const int m = blockIdx.x * (256 >> tlog2) + (threadIdx.x >> tlog2);
@@ -191,7 +200,7 @@ __global__ __launch_bounds__(256) void k_mmvh(const uint8_t* __restrict__ w, int
     if (T <= 64) {
         if (t == 0 && m < M) {
 #pragma unroll
-            for (int c = 0; c < B; ++c) y[size_t(c) * M + m] = acc[c];
+            for (int c = 0; c < B; ++c) y[size_t(c) * ycol + m] = acc[c];
         }
         return;
     }
@@ -206,17 +215,17 @@ __global__ __launch_bounds__(256) void k_mmvh(const uint8_t* __restrict__ w, int
         for (int c = 0; c < B; ++c) {
             float s = 0.0f;
             for (int i = 0; i < waves; ++i) s += red[wave + i][c];
-            y[size_t(c) * M + m] = s;
+            y[size_t(c) * ycol + m] = s;
         }
     }
 }
 
 template <int TYPE>
 hipError_t launch_type(int B, const uint8_t* w, int64_t nb01, int M, int K, int tl, const __half2* h,
-                       const float2* meta, float* y, hipStream_t stream) {
-    const dim3 grid((M + (256 >> tl) - 1) / (256 >> tl));
+                       const float2* meta, float* y, hipStream_t stream, const Slices& sl) {
+    const dim3 grid((M + (256 >> tl) - 1) / (256 >> tl), sl.ne12, sl.ne13);
 #define P1X_CASE(N) \
-    case N: hipLaunchKernelGGL((k_mmvh<TYPE, N>), grid, dim3(256), 0, stream, w, nb01, M, K, tl, h, meta, y); break;
+    case N: hipLaunchKernelGGL((k_mmvh<TYPE, N>), grid, dim3(256), 0, stream, w, nb01, M, K, tl, h, meta, y, sl); break;
     switch (B) {
         P1X_CASE(1) P1X_CASE(2) P1X_CASE(3) P1X_CASE(4) P1X_CASE(5) P1X_CASE(6) P1X_CASE(7) P1X_CASE(8)
         default: return hipErrorInvalidValue;
@@ -236,16 +245,16 @@ int mmvh_threads_log2(int M, int K) {
 }
 
 hipError_t launch_mmvh(int type, int B, const void* w, int64_t nb01, int M, int K, const uint16_t* h,
-                       const float* meta, float* y, hipStream_t stream) {
+                       const float* meta, float* y, hipStream_t stream, const Slices& sl) {
     const int tl = mmvh_threads_log2(M, K);
     const auto* wb = static_cast<const uint8_t*>(w);
     const auto* h2 = reinterpret_cast<const __half2*>(h);
     const auto* m2 = reinterpret_cast<const float2*>(meta);
     switch (type) {
-        case Q4_0: return launch_type<Q4_0>(B, wb, nb01, M, K, tl, h2, m2, y, stream);
-        case Q8_0: return launch_type<Q8_0>(B, wb, nb01, M, K, tl, h2, m2, y, stream);
-        case Q4_K: return launch_type<Q4_K>(B, wb, nb01, M, K, tl, h2, m2, y, stream);
-        case Q6_K: return launch_type<Q6_K>(B, wb, nb01, M, K, tl, h2, m2, y, stream);
+        case Q4_0: return launch_type<Q4_0>(B, wb, nb01, M, K, tl, h2, m2, y, stream, sl);
+        case Q8_0: return launch_type<Q8_0>(B, wb, nb01, M, K, tl, h2, m2, y, stream, sl);
+        case Q4_K: return launch_type<Q4_K>(B, wb, nb01, M, K, tl, h2, m2, y, stream, sl);
+        case Q6_K: return launch_type<Q6_K>(B, wb, nb01, M, K, tl, h2, m2, y, stream, sl);
     }
     return hipErrorInvalidValue;
 }

@@ -313,7 +313,8 @@ __device__ __forceinline__ void copy_to_lds(const int8_t* __restrict__ qs, const
 // `prep`, so the weight stream and the activation copy share one memory round trip.
 template <int TYPE, int B, int RW, bool SUMS, bool HOIST = false, class Act, class Prep>
 __device__ __forceinline__ void mmvq_rows(const Act act, Prep prep, const uint8_t* __restrict__ w, int64_t nb01,
-                                          int M, int K, float* __restrict__ y, int32_t* __restrict__ gs) {
+                                          int M, int K, float* __restrict__ y, int32_t* __restrict__ gs,
+                                          int64_t ycol) {
     using U = typename UnitOf<TYPE>::T;
     constexpr int UB = units_per_lane<TYPE, B>();
     constexpr int kStep = 64 * UB;  // units per pass
@@ -395,7 +396,7 @@ __device__ __forceinline__ void mmvq_rows(const Act act, Prep prep, const uint8_
 #pragma unroll
         for (int c = 0; c < B; ++c) {
             const float t = wave_total(acc[r][c]);
-            if (lane == 0 && r0 + r < M) y[size_t(c) * M + r0 + r] = t;
+            if (lane == 0 && r0 + r < M) y[size_t(c) * ycol + r0 + r] = t;
         }
     }
 }
@@ -413,7 +414,16 @@ struct LdsAct {
 template <int TYPE, int B, int RW, bool SUMS, bool LDS>
 __global__ __launch_bounds__(256) void k_mmvq(const uint8_t* __restrict__ w, int64_t nb01, int M, int K,
                                               const int8_t* __restrict__ xq, const float4* __restrict__ xds,
-                                              float* __restrict__ y, int32_t* __restrict__ gs) {
+                                              float* __restrict__ y, int32_t* __restrict__ gs, const Slices sl) {
+    if (gridDim.y * gridDim.z > 1) {  // a batched launch: this work-group's slice (wave-uniform)
+        const int i2 = blockIdx.y, i3 = blockIdx.z;
+        w += (i2 / sl.r2) * sl.w2 + (i3 / sl.r3) * sl.w3;
+        const int64_t col0 = (int64_t(i3) * sl.ne12 + i2) * B;
+        xq += col0 * K;
+        xds += col0 * (K / 32);
+        y += i2 * sl.y2 + i3 * sl.y3;
+    }
+    const int64_t ycol = sl.ycol ? sl.ycol : M;
     if constexpr (LDS) {
         extern __shared__ uint4 act_lds[];
         const int nblk = K / 32;
@@ -424,9 +434,9 @@ __global__ __launch_bounds__(256) void k_mmvq(const uint8_t* __restrict__ w, int
                 copy_to_lds<B>(xq, xds, K, l.lo, l.hi, l.ds);
                 __syncthreads();
             },
-            w, nb01, M, K, y, gs);
+            w, nb01, M, K, y, gs, ycol);
     } else {
-        mmvq_rows<TYPE, B, RW, SUMS>(ActGlobal{xq, xds, K}, [] {}, w, nb01, M, K, y, gs);
+        mmvq_rows<TYPE, B, RW, SUMS>(ActGlobal{xq, xds, K}, [] {}, w, nb01, M, K, y, gs, ycol);
     }
 }
 
@@ -445,7 +455,7 @@ __global__ __launch_bounds__(256) void k_mmvq_fx(const uint8_t* __restrict__ w, 
             quantize_to_lds<B>(x, K, l.lo, l.hi, l.ds);
             __syncthreads();
         },
-        w, nb01, M, K, y, gs);
+        w, nb01, M, K, y, gs, M);
 }
 
 // One activation column on a prepared Q8_1 activation (q4_0 / q8_0): the activation stays in registers. A row-group
@@ -927,12 +937,13 @@ hipError_t launch_mmvr_cols(const MmvrPlan& p, int B, const uint8_t* w, int64_t 
 
 template <int TYPE, int B>
 hipError_t launch_b(const uint8_t* w, int64_t nb01, int M, int K, int rw, const int8_t* xq, const float4* xds,
-                    const float* x, float* y, int32_t* gs, hipStream_t stream) {
+                    const float* x, float* y, int32_t* gs, hipStream_t stream, const Slices& sl) {
     // The group-sum export runs the same rows per wave as the plain launch, so a check with sums exercises the
     // instantiation the shape dispatches. The single-launch form quantizes x itself; it serves one column (p1x_mul_mat_vec takes the Q8_1 pass and the
     // prepared kernels from two columns on).
     if (x && B != 1) return hipErrorInvalidValue;
-    const dim3 grid((M + 4 * rw - 1) / (4 * rw));
+    if (x && (sl.ne12 != 1 || sl.ne13 != 1)) return hipErrorInvalidValue;
+    const dim3 grid((M + 4 * rw - 1) / (4 * rw), sl.ne12, sl.ne13);
     const size_t lds = size_t(48) * B * (K / 32);
     const bool use_lds = lds <= 65536;
 #define P1X_RW(R)                                                                                                  \
@@ -951,16 +962,16 @@ hipError_t launch_b(const uint8_t* w, int64_t nb01, int M, int K, int rw, const 
         }                                                                                                          \
         if (gs && use_lds)                                                                                         \
             hipLaunchKernelGGL((k_mmvq<TYPE, B, R, true, true>), grid, dim3(256), lds, stream, w, nb01, M, K, xq, xds, y, \
-                               gs);                                                                                \
+                               gs, sl);                                                                                \
         else if (gs)                                                                                               \
             hipLaunchKernelGGL((k_mmvq<TYPE, B, R, true, false>), grid, dim3(256), 0, stream, w, nb01, M, K, xq, xds, y, \
-                               gs);                                                                                \
+                               gs, sl);                                                                                \
         else if (use_lds)                                                                                          \
             hipLaunchKernelGGL((k_mmvq<TYPE, B, R, false, true>), grid, dim3(256), lds, stream, w, nb01, M, K, xq, xds, \
-                               y, gs);                                                                             \
+                               y, gs, sl);                                                                             \
         else                                                                                                       \
             hipLaunchKernelGGL((k_mmvq<TYPE, B, R, false, false>), grid, dim3(256), 0, stream, w, nb01, M, K, xq, xds, \
-                               y, gs);                                                                             \
+                               y, gs, sl);                                                                             \
         return hipGetLastError();                                                                                  \
     }
     P1X_RW(1)
@@ -972,16 +983,17 @@ hipError_t launch_b(const uint8_t* w, int64_t nb01, int M, int K, int rw, const 
 
 template <int TYPE>
 hipError_t launch_type(int B, const uint8_t* w, int64_t nb01, int M, int K, int rw, const int8_t* xq,
-                       const float4* xds, const float* x, float* y, int32_t* gs, hipStream_t stream) {
+                       const float4* xds, const float* x, float* y, int32_t* gs, hipStream_t stream,
+                       const Slices& sl = Slices{}) {
     switch (B) {
-        case 1: return launch_b<TYPE, 1>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream);
-        case 2: return launch_b<TYPE, 2>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream);
-        case 3: return launch_b<TYPE, 3>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream);
-        case 4: return launch_b<TYPE, 4>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream);
-        case 5: return launch_b<TYPE, 5>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream);
-        case 6: return launch_b<TYPE, 6>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream);
-        case 7: return launch_b<TYPE, 7>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream);
-        case 8: return launch_b<TYPE, 8>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream);
+        case 1: return launch_b<TYPE, 1>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream, sl);
+        case 2: return launch_b<TYPE, 2>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream, sl);
+        case 3: return launch_b<TYPE, 3>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream, sl);
+        case 4: return launch_b<TYPE, 4>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream, sl);
+        case 5: return launch_b<TYPE, 5>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream, sl);
+        case 6: return launch_b<TYPE, 6>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream, sl);
+        case 7: return launch_b<TYPE, 7>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream, sl);
+        case 8: return launch_b<TYPE, 8>(w, nb01, M, K, rw, xq, xds, x, y, gs, stream, sl);
     }
     return hipErrorInvalidValue;
 }
@@ -1024,6 +1036,20 @@ hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int 
         case Q8_0: return launch_type<Q8_0>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
         case Q4_K: return launch_type<Q4_K>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
         case Q6_K: return launch_type<Q6_K>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_mmvq_batched(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq,
+                               const float* xds, float* y, const Slices& sl, hipStream_t stream) {
+    const int rw = mmvq_rows_per_wave(M, B, false);
+    const auto* wb = static_cast<const uint8_t*>(w);
+    const auto* d4 = reinterpret_cast<const float4*>(xds);
+    switch (type) {
+        case Q4_0: return launch_type<Q4_0>(B, wb, nb01, M, K, rw, xq, d4, nullptr, y, nullptr, stream, sl);
+        case Q8_0: return launch_type<Q8_0>(B, wb, nb01, M, K, rw, xq, d4, nullptr, y, nullptr, stream, sl);
+        case Q4_K: return launch_type<Q4_K>(B, wb, nb01, M, K, rw, xq, d4, nullptr, y, nullptr, stream, sl);
+        case Q6_K: return launch_type<Q6_K>(B, wb, nb01, M, K, rw, xq, d4, nullptr, y, nullptr, stream, sl);
     }
     return hipErrorInvalidValue;
 }
