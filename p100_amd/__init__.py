@@ -37,7 +37,7 @@ EXPORTS = ["p1x_version", "p1x_init", "p1x_last_error", "p1x_quantize_q8_1", "p1
            "p1x_flash_attn_decode_kvlen", "p1x_round_to_fp16", "p1x_get_rows", "p1x_rms_norm_q8_1", "p1x_rms_norm_mul_mat_vec",
            "p1x_swiglu_q8_1",
            "p1x_rope_kv_append", "p1x_argmax_workspace", "p1x_argmax", "p1x_llama_workspace", "p1x_llama_decode_step",
-           "p1x_flash_attn_decode_quant", "p1x_flash_attn_decode_noalloc", "p1x_read_bytes",
+           "p1x_flash_attn_decode_quant", "p1x_flash_attn_decode_noalloc", "p1x_read_bytes", "p1x_fa_select_kernel",
            "p1x_should_use_mmvh", "p1x_mul_mat_vec_batched_workspace", "p1x_mul_mat_vec_batched"]
 
 
@@ -112,6 +112,7 @@ def load():
         "p1x_flash_attn_decode_noalloc": (C.c_int, [C.POINTER(AttnParams), vp, vp, vp, C.POINTER(KVStrides), vp, vp,
                                                     vp, vp, vp]),
         "p1x_read_bytes": (C.c_int, [vp, sz, vp, C.c_int, vp]),
+        "p1x_fa_select_kernel": (C.c_int, [C.c_int]),
         "p1x_round_to_fp16": (C.c_int, [vp, vp, i64, vp]),
         "p1x_get_rows": (C.c_int, [C.c_int, vp, i64, i64, i64, vp, vp, vp]),
         "p1x_rms_norm_q8_1": (C.c_int, [vp, vp, vp, i64, C.c_float, vp, vp, vp, vp]),
@@ -293,6 +294,16 @@ def validate(p: AttnParams) -> str:
     lib = load()
     p = _params(p)
     return "" if lib.p1x_attn_validate(C.byref(p)) == OK else lib.p1x_last_error().decode()
+
+
+FA_KERNEL = {"auto": 0, "split": 1, "mc": 2}  # P1X_FA_KERNEL_AUTO / _SPLIT / _MC
+
+
+def fa_select_kernel(kernel: str) -> None:
+    """The decode attention's first-pass kernel for the process: "auto", "split" (vector) or "mc" (matrix cores)."""
+    lib = load()
+    if lib.p1x_fa_select_kernel(FA_KERNEL[kernel]) != OK:
+        raise ValueError(lib.p1x_last_error().decode())
 
 
 def flash_attn_decode_workspace(p: AttnParams) -> int:

@@ -109,11 +109,16 @@ const char* attn_reason(const p1x_attn_params* p) {
     return nullptr;
 }
 
+// Partials of the larger of the fp16 and the quantized-cache plans (one workspace serves both entry points).
 size_t fa_workspace(const p1x_attn_params* p) {
     if (!p || attn_reason(p)) return 0;
-    int splits = 0, chunk = 0;
-    fa_split_plan(p->batch, p->n_head_q, p->n_head_kv, p->seq_q, p->seq_kv, p->d_qk, splits, chunk);
-    return splits == 1 ? 0 : size_t(p->batch) * p->n_head_q * p->seq_q * splits * (p->d_v + 2) * sizeof(float);
+    size_t need = 0;
+    for (bool f16 : {true, false}) {
+        const p1x::FaPlan pl = p1x::fa_plan(p->batch, p->n_head_q, p->n_head_kv, p->seq_q, p->seq_kv, p->d_qk, f16);
+        const size_t n = pl.splits == 1 ? 0 : size_t(p->batch) * p->n_head_q * p->seq_q * pl.splits * (p->d_v + 2) * 4;
+        need = n > need ? n : need;
+    }
+    return need;
 }
 
 int fa_prepare(const p1x_attn_params* p, const float* q, const uint16_t* k, const uint16_t* v,
@@ -123,7 +128,8 @@ int fa_prepare(const p1x_attn_params* p, const float* q, const uint16_t* k, cons
     if (!q || !k || !v || !o) return fail(P1X_EINVAL, "null q, k, v or o pointer");
     if (p->d_qk != p->d_v || (p->d_qk != 64 && p->d_qk != 128 && p->d_qk != 256))
         return fail(P1X_EUNSUPPORTED, "decode kernel supports d_qk == d_v in {64, 128, 256}");
-    const int64_t head_chunks = (p->n_head_q / p->n_head_kv) / fa_heads_per_wg(p->n_head_q, p->n_head_kv);
+    const p1x::FaPlan plan = p1x::fa_plan(p->batch, p->n_head_q, p->n_head_kv, p->seq_q, p->seq_kv, p->d_qk, kv_f16);
+    const int64_t head_chunks = plan.head_chunks;
     if (p->seq_q > 65535 || int64_t(p->batch) * p->n_head_kv * head_chunks > 65535)
         return fail(P1X_EUNSUPPORTED, "seq_q and batch*n_head_kv*(query heads per KV head / heads per group) must be <= 65535");
     if (!aligned(q, 16) || (kv_f16 && (!aligned(k, 16) || !aligned(v, 16))))
@@ -164,8 +170,12 @@ int fa_prepare(const p1x_attn_params* p, const float* q, const uint16_t* k, cons
     a.causal = p->causal != 0;
     a.scale = p->scale == 0.0f ? 1.0f / std::sqrt(float(p->d_qk)) : p->scale;
     a.softcap = p->softcap;
-    fa_split_plan(p->batch, p->n_head_q, p->n_head_kv, p->seq_q, p->seq_kv, p->d_qk, a.splits, a.chunk);
-    const size_t need = fa_workspace(p);
+    a.splits = plan.splits;
+    a.chunk = plan.chunk;
+    a.nh = plan.nh;
+    a.head_chunks = int(plan.head_chunks);
+    a.mc = plan.mc ? 1 : 0;
+    const size_t need = plan.splits == 1 ? 0 : size_t(p->batch) * p->n_head_q * p->seq_q * plan.splits * (d + 2) * 4;
     if (need && (!ws || ws_bytes < need))
         return fail(P1X_EWORKSPACE, "workspace of " + std::to_string(need) + " bytes required");
     if (need && !aligned(ws, 16)) return fail(P1X_EINVAL, "workspace must be 16-byte aligned");
@@ -483,6 +493,13 @@ int p1x_read_bytes(const void* src, size_t bytes, uint32_t* digest, int work_gro
     if (work_groups < 1 || work_groups > 65536) return fail(P1X_EINVAL, "work_groups must be 1..65536");
     hipError_t e = p1x::launch_read_bytes(src, int64_t(bytes), digest, work_groups, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? P1X_OK : hip_fail(e, "read_bytes");
+}
+
+int p1x_fa_select_kernel(int kernel) {
+    if (kernel < P1X_FA_KERNEL_AUTO || kernel > P1X_FA_KERNEL_MC)
+        return fail(P1X_EINVAL, "kernel must be P1X_FA_KERNEL_AUTO, _SPLIT or _MC");
+    p1x::fa_select_kernel(kernel);
+    return P1X_OK;
 }
 
 }  // extern "C"

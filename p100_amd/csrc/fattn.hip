@@ -22,6 +22,7 @@
 // and LSE itself and pass 2 is skipped.
 // (A single launch, where the last work-group to arrive combines, needs an agent-scope release per work-group:
 // each one writes back the XCD's L2, and one per work-group alone costs more than the second launch.)
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 
@@ -641,16 +642,288 @@ __global__ __launch_bounds__(64) void k_fa_combine(FaArgs a) {
     if (a.oq) q8_1_row<CPL>(ov, size_t(row) * D + CPL * lane, a.oq, a.ods);
 }
 
-template <int D, int NH, int KT>
-hipError_t launch_split(const FaArgs& a, int batch, hipStream_t stream) {
-    const dim3 grid(a.splits, batch * a.hkv * a.head_chunks, a.seq_q);
-    switch ((a.mask ? 1 : 0) | (a.softcap > 0.0f ? 2 : 0)) {
-        case 0: hipLaunchKernelGGL((k_fa_split<D, NH, 0, KT>), grid, dim3(kSplitThreads), 0, stream, a); break;
-        case 1: hipLaunchKernelGGL((k_fa_split<D, NH, 1, KT>), grid, dim3(kSplitThreads), 0, stream, a); break;
-        case 2: hipLaunchKernelGGL((k_fa_split<D, NH, 2, KT>), grid, dim3(kSplitThreads), 0, stream, a); break;
-        default: hipLaunchKernelGGL((k_fa_split<D, NH, 3, KT>), grid, dim3(kSplitThreads), 0, stream, a); break;
+// ------------------------------------------------------------------------------------------- matrix-core split pass
+// fp16 K/V with d = 128 (the decode configuration): the same split, partials and combine as k_fa_split, with the
+// logits on matrix cores. A work-group holds NH query heads of one KV head (the whole GQA group when it divides by
+// 4, so K and V are read once) and 4 waves; wave w takes 16-key blocks j0 + 64 t + 16 w + (0..15).
+//  * Q.K^T: one v_mfma_f32_16x16x32_f16 per 32 dimensions. B is K^T: lane l holds key (l % 16)'s dimensions
+//    32 m + 8 (l / 16) .. + 7 for step m, so each 16-byte load instruction reads 64 contiguous bytes of 16 rows;
+//    A holds the same dimensions of query head (l % 16) (rows >= NH are zero). Q is scaled by a power of two into fp16 range and split into fp16 hi + lo
+//    parts, two products per step, so the logits keep FP32 accuracy (exact fp16 products, FP32 accumulation). The
+//    result leaves lane i < 16 holding the NH logits of key i: no cross-lane reduction per key.
+//  * softmax: the wave's lazy reference max per head (raised, with a rescale, only when a block exceeds it by more
+//    than kTau), p = 2^(x - ref) in lanes 0..15, moved to scalar registers with readlane.
+//  * P.V: lane l owns dimensions 2l and 2l + 1 of every head's accumulator; each V row of the block is one 256-byte
+//    dword load across the wave, multiplied by the scalar p of its key (v_fma_mix, fp16 V promoted in the FMA), so
+//    the accumulator needs no reduction at the end.
+// Loads are range-checked buffer loads (keys at or past the share's end, and blocks past the wave's last, read
+// zeros and touch no memory), issued PF blocks ahead of use.
+#ifndef P1X_FA_MC_PF
+#define P1X_FA_MC_PF 2  // 16-key blocks in flight per wave
+#endif
+#ifndef P1X_FA_MC_OCC
+#define P1X_FA_MC_OCC 2  // waves per SIMD the register budget allows
+#endif
+#ifndef P1X_FA_MC_WAVES
+#define P1X_FA_MC_WAVES 4  // waves per work-group: a work-group takes 16 * P1X_FA_MC_WAVES keys per round
+#endif
+constexpr int kMcWaves = P1X_FA_MC_WAVES;
+typedef _Float16 mc_h8 __attribute__((ext_vector_type(8)));
+typedef float mc_f4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float row_max16(float v) {  // max over each 16-lane row, every lane of the row gets it
+    v = fmaxf(v, dpp_f<kXor1>(v));
+    v = fmaxf(v, dpp_f<kXor2>(v));
+    v = fmaxf(v, dpp_f<kHalfMirror>(v));
+    return fmaxf(v, dpp_f<kMirror>(v));
+}
+__device__ __forceinline__ float row_sum16(float v) {
+    v += dpp_f<kXor1>(v);
+    v += dpp_f<kXor2>(v);
+    v += dpp_f<kHalfMirror>(v);
+    return v + dpp_f<kMirror>(v);
+}
+
+template <int NH, int MODE>
+__global__ __launch_bounds__(64 * kMcWaves, P1X_FA_MC_OCC) void k_fa_mc(FaArgs a) {
+    constexpr int D = 128, W = kMcWaves, KPB = 16 * W, PF = P1X_FA_MC_PF;
+    constexpr bool kMask = (MODE & 1) != 0, kCap = (MODE & 2) != 0;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+    const int ki = lane & 15, g = lane >> 4;
+    const int split = blockIdx.x;
+    int kvh_all, b, kvh;
+    if (a.head_chunks == 1) kvh_all = blockIdx.y;
+    else if (a.head_chunks == 2) kvh_all = int(blockIdx.y) >> 1;
+    else kvh_all = int(blockIdx.y) / a.head_chunks;
+    const int hc = blockIdx.y - kvh_all * a.head_chunks;
+    if (kvh_all < a.hkv) b = 0, kvh = kvh_all;
+    else b = kvh_all / a.hkv, kvh = kvh_all - b * a.hkv;
+    const int i = blockIdx.z;
+    const int h0 = (kvh * a.head_chunks + hc) * NH;
+
+    const int n_kv = a.kv_len ? min(max(*a.kv_len, 0), a.seq_kv) : a.seq_kv;
+    const int j_end = a.causal ? min(n_kv, i + (n_kv - a.seq_q) + 1) : n_kv;
+    int chunk = a.chunk;
+    if (a.kv_len) chunk = ceil_div_uniform(n_kv, a.splits * KPB) * KPB;
+    const int j0 = split * chunk;
+    const int j1 = min(j0 + chunk, j_end);
+    const int nb = j1 > j0 ? (j1 - j0 + KPB - 1) / KPB : 0;  // blocks per wave (the last may hold no valid key)
+
+    // The resources end with row j1 - 1 of the share, and keys at or past j1 (blocks past the wave's last
+    // included) are clamped to row j1, whose offset (rows are at least D elements apart) lies past that end: every
+    // such load reads zeros, with no per-key selects. (Uniform selects of load offsets become branches whose
+    // merges force a wait for all loads in flight, serialising the ring.)
+    const uint32_t krow = uint32_t(a.k_row) * 2, vrow = uint32_t(a.v_row) * 2;
+    const auto share_end = [&](uint32_t row, uint32_t whole) {
+        return j1 > j0 ? min(whole, uint32_t(j1 - 1) * row + 2 * D) : 0u;
+    };
+    const auto krs = kv_rsrc(a.k + size_t(b) * a.k_batch + size_t(kvh) * a.k_head, share_end(krow, a.k_bytes));
+    const auto vrs = kv_rsrc(a.v + size_t(b) * a.v_batch + size_t(kvh) * a.v_head, share_end(vrow, a.v_bytes));
+    // The mask row, read with the block it belongs to (a load issued later would wait for the whole ring).
+    const auto mrs = __builtin_amdgcn_make_buffer_rsrc(kMask ? const_cast<float*>(a.mask + size_t(i) * a.seq_kv) : nullptr,
+                                                      (short)0, kMask && j1 > j0 ? j1 * 4 : 0, 0x00020000);
+    struct Blk {
+        uint4 k[4];
+        uint32_t v[16];
+        float mk;  // the mask of key kb + (lane % 16)
+    };
+    const uint32_t k_lane = uint32_t(8 * g) * 2, v_lane = uint32_t(2 * lane) * 2;
+    auto load_k = [&](Blk& bk, int t) {
+        const int kb = j0 + t * KPB + 16 * wave;  // wave-uniform
+        // A plain 32-bit product: fused into v_mad_u64_u32, its undefined high addend can land in a register
+        // still awaiting a load, and the compiler then waits for every load in flight.
+        uint32_t ko = uint32_t(min(kb + ki, j1)) * krow;
+        asm volatile("" : "+v"(ko));
+        ko += k_lane;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) bk.k[m] = ld_kv(krs, ko + 64 * m);
+        if constexpr (kMask)
+            bk.mk = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(mrs, uint32_t(min(kb + ki, j1)) * 4, 0, 0));
+    };
+    auto load_v = [&](Blk& bk, int t, int k) {
+        const int kb = j0 + t * KPB + 16 * wave;
+        bk.v[k] = __builtin_amdgcn_raw_buffer_load_b32(vrs, uint32_t(min(kb + k, j1)) * vrow + v_lane, 0, P1X_FA_AUX);
+    };
+    auto load = [&](Blk& bk, int t) {
+        load_k(bk, t);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) load_v(bk, t, k);
+    };
+    __shared__ float4 pbuf[W][16];  // each wave's p of its current block, 4 heads per key
+    float mref[NH], s[NH], o[NH][2];
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+        mref[h] = -INFINITY;
+        s[h] = 0.0f;
+        o[h][0] = o[h][1] = 0.0f;
     }
-    if (a.splits == 1) return hipGetLastError();  // the split pass wrote O and LSE
+    // Q: lane (head ki < NH, dims 32 m + 8 g .. + 7 as qv[8 m ..]), scaled into base 2 (or kept natural for the
+    // softcap). Q and the first PF blocks are all requested before any of them is used (the scheduling barrier
+    // keeps the compiler from placing the Q arithmetic, and its wait, between the block loads).
+    float4 qraw[8];
+    {
+        const float* qp = a.q + ((size_t(b) * a.hq + h0 + min(ki, NH - 1)) * a.seq_q + i) * D + 8 * g;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) qraw[c] = reinterpret_cast<const float4*>(qp + 32 * (c >> 1))[c & 1];
+    }
+    Blk ring[PF];
+#pragma unroll
+    for (int q = 0; q < PF; ++q) load(ring[q], q);
+    __builtin_amdgcn_sched_barrier(0);
+    const float qmul = kCap ? a.scale : a.scale * kLog2e;
+    float qv[32];
+    float qmax = 0.0f;
+    {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const float4 t = qraw[c];
+            qv[4 * c] = t.x * qmul, qv[4 * c + 1] = t.y * qmul, qv[4 * c + 2] = t.z * qmul, qv[4 * c + 3] = t.w * qmul;
+        }
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+            qv[e] = ki < NH ? qv[e] : 0.0f;
+            qmax = fmaxf(qmax, fabsf(qv[e]));
+        }
+    }
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 16));
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 32));  // lanes ki, ki + 16, 32, 48: head ki's largest |q|
+    int qexp = 0;
+    (void)frexpf(qmax, &qexp);  // qmax < 2^qexp
+    const float up = qmax > 0.0f ? ldexpf(1.0f, 14 - qexp) : 1.0f;  // |q * up| < 2^14: fp16 range, exact scale
+    mc_h8 qhi[4], qlo[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float x = qv[8 * m + j] * up;
+            const _Float16 hi = static_cast<_Float16>(x);
+            qhi[m][j] = hi;
+            qlo[m][j] = static_cast<_Float16>(x - static_cast<float>(hi));
+        }
+    float down[NH];  // 1 / up of each head, wave-uniform
+#pragma unroll
+    for (int h = 0; h < NH; ++h)
+        down[h] = 1.0f / __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, up), h));
+
+    // Block t from bk; with `refill`, each register of bk is reloaded with block tn as soon as it has been used
+    // (K after the products, each V row after its accumulation), so the loads in flight stay level instead of
+    // draining once per block.
+    auto compute = [&](Blk& bk, int t, int tn, bool refill) {
+        mc_f4 chi = {0.0f, 0.0f, 0.0f, 0.0f}, clo = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const mc_h8 kh = __builtin_bit_cast(mc_h8, bk.k[m]);
+            chi = __builtin_amdgcn_mfma_f32_16x16x32_f16(qhi[m], kh, chi, 0, 0, 0);
+            clo = __builtin_amdgcn_mfma_f32_16x16x32_f16(qlo[m], kh, clo, 0, 0, 0);
+        }
+        const float mk = kMask ? bk.mk : 0.0f;
+        if (refill) load_k(bk, tn);
+        const int key = j0 + t * KPB + 16 * wave + ki;
+        const bool ok = lane < 16 && key < j1;  // lanes 0..15 hold rows 0..3 (the heads) of key ki
+        float x[NH];
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+            float v = (chi[h] + clo[h]) * down[h];
+            if constexpr (kCap || kMask) {
+                const float add = kMask && ok ? mk : 0.0f;
+                v = kCap ? (a.softcap * tanhf(v / a.softcap) + add) * kLog2e : v + add * kLog2e;
+            }
+            x[h] = ok ? v : -INFINITY;
+        }
+        // Does any logit exceed its head's reference by more than kTau? One compare per head and a ballot; the
+        // block maxima are reduced only then (rarely: the reference moves O(log) times over a row).
+        bool hi = false;
+#pragma unroll
+        for (int h = 0; h < NH; ++h) hi |= x[h] > mref[h] + kTau;  // -inf logits never pass; -inf + kTau = -inf
+        if (__builtin_amdgcn_ballot_w64(hi) != 0) {  // wave-uniform: raise each reference to its block max, rescale
+#pragma unroll
+            for (int h = 0; h < NH; ++h) {
+                const float bm = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, row_max16(x[h]))));
+                const float mn = fmaxf(mref[h], bm);
+                const float alpha = mref[h] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mref[h] - mn);
+                s[h] *= alpha;
+                o[h][0] *= alpha;
+                o[h][1] *= alpha;
+                mref[h] = mn;
+            }
+        }
+        float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+            const float base = mref[h] == -INFINITY ? 0.0f : mref[h];
+            p[h] = __builtin_amdgcn_exp2f(x[h] - base);
+            s[h] += p[h];
+        }
+        // The block's p (key ki in lane ki < 16) to every lane: one 16-byte LDS write per key, then broadcast reads
+        // (one address per instruction). LDS operations of a wave are performed in order, so the wave's own slot
+        // needs no barrier; the scheduling barrier keeps the compiler from moving the reads above the write.
+        if (lane < 16) pbuf[wave][lane] = make_float4(p[0], p[1], p[2], p[3]);
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const float4 pk4 = pbuf[wave][k];
+            const float pk[4] = {pk4.x, pk4.y, pk4.z, pk4.w};
+            const __half2 vv = __builtin_bit_cast(__half2, bk.v[k]);
+            const float v0 = __low2float(vv), v1 = __high2float(vv);
+#pragma unroll
+            for (int h = 0; h < NH; ++h) {
+                o[h][0] = fmaf(pk[h], v0, o[h][0]);
+                o[h][1] = fmaf(pk[h], v1, o[h][1]);
+            }
+            if (refill) load_v(bk, tn, k);
+        }
+        __builtin_amdgcn_wave_barrier();  // the next block's write follows every read of this one
+    };
+    int t0 = 0;
+    for (; t0 + PF <= nb; t0 += PF) {
+#pragma unroll
+        for (int q = 0; q < PF; ++q) compute(ring[q], t0 + q, t0 + q + PF, true);
+    }
+#pragma unroll
+    for (int q = 0; q < PF - 1; ++q)
+        if (t0 + q < nb) compute(ring[q], t0 + q, 0, false);
+
+    // Per wave: the sum of p over its keys (lanes 0..15), then the W waves merged at their common max.
+    __shared__ float wm[W][NH], wsum[W][NH], wo[W][NH][D];
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+        const float st = row_sum16(s[h]);
+        if (lane == 0) {
+            wm[wave][h] = mref[h];
+            wsum[wave][h] = st;
+        }
+        *reinterpret_cast<float2*>(&wo[wave][h][2 * lane]) = make_float2(o[h][0], o[h][1]);
+    }
+    __syncthreads();
+    const int grp = blockIdx.y * a.seq_q + i;
+    const size_t row0 = (size_t(b) * a.hq + h0) * a.seq_q + i;
+    for (int idx = threadIdx.x; idx < NH * D; idx += 64 * W) {
+        const int hh = idx / D, d = idx % D;
+        float mx = wm[0][hh];
+#pragma unroll
+        for (int w = 1; w < W; ++w) mx = fmaxf(mx, wm[w][hh]);
+        float num = 0.0f, den = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const float wt = wm[w][hh] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(wm[w][hh] - mx);
+            num = fmaf(wt, wo[w][hh][d], num);
+            den = fmaf(wt, wsum[w][hh], den);
+        }
+        if (a.splits == 1) {
+            const size_t row = row0 + size_t(hh) * a.seq_q;
+            a.o[row * D + d] = den == 0.0f ? 0.0f : num / den;
+            if (a.lse && d == 0) a.lse[row] = den == 0.0f ? -INFINITY : (mx + log2f(den)) * kLn2;
+        } else {
+            const size_t pr = (size_t(grp) * a.splits + split) * NH + hh;
+            a.part_o[pr * D + d] = num;
+            if (d == 0) a.part_ml[pr] = make_float2(mx, den);
+        }
+    }
+}
+
+template <int D, int NH>
+hipError_t launch_combine(const FaArgs& a, int batch, hipStream_t stream) {
     // Splits per round of partial loads: the smallest of 8, 16, 32 covering the plan (loads past the last split
     // repeat a valid row with weight 0, so a round sized to the plan issues no wasted requests); split statistics
     // in one register up to 64 splits.
@@ -664,6 +937,32 @@ hipError_t launch_split(const FaArgs& a, int batch, hipStream_t stream) {
     else
         hipLaunchKernelGGL((k_fa_combine<D, NH, 32, kMaxSplits / 64>), cgrid, dim3(64), 0, stream, a);
     return hipGetLastError();
+}
+
+template <int NH>
+hipError_t launch_mc(const FaArgs& a, int batch, hipStream_t stream) {
+    const dim3 grid(a.splits, batch * a.hkv * a.head_chunks, a.seq_q);
+    switch ((a.mask ? 1 : 0) | (a.softcap > 0.0f ? 2 : 0)) {
+        case 0: hipLaunchKernelGGL((k_fa_mc<NH, 0>), grid, dim3(64 * kMcWaves), 0, stream, a); break;
+        case 1: hipLaunchKernelGGL((k_fa_mc<NH, 1>), grid, dim3(64 * kMcWaves), 0, stream, a); break;
+        case 2: hipLaunchKernelGGL((k_fa_mc<NH, 2>), grid, dim3(64 * kMcWaves), 0, stream, a); break;
+        default: hipLaunchKernelGGL((k_fa_mc<NH, 3>), grid, dim3(64 * kMcWaves), 0, stream, a); break;
+    }
+    if (a.splits == 1) return hipGetLastError();  // the split pass wrote O and LSE
+    return launch_combine<128, NH>(a, batch, stream);
+}
+
+template <int D, int NH, int KT>
+hipError_t launch_split(const FaArgs& a, int batch, hipStream_t stream) {
+    const dim3 grid(a.splits, batch * a.hkv * a.head_chunks, a.seq_q);
+    switch ((a.mask ? 1 : 0) | (a.softcap > 0.0f ? 2 : 0)) {
+        case 0: hipLaunchKernelGGL((k_fa_split<D, NH, 0, KT>), grid, dim3(kSplitThreads), 0, stream, a); break;
+        case 1: hipLaunchKernelGGL((k_fa_split<D, NH, 1, KT>), grid, dim3(kSplitThreads), 0, stream, a); break;
+        case 2: hipLaunchKernelGGL((k_fa_split<D, NH, 2, KT>), grid, dim3(kSplitThreads), 0, stream, a); break;
+        default: hipLaunchKernelGGL((k_fa_split<D, NH, 3, KT>), grid, dim3(kSplitThreads), 0, stream, a); break;
+    }
+    if (a.splits == 1) return hipGetLastError();  // the split pass wrote O and LSE
+    return launch_combine<D, NH>(a, batch, stream);
 }
 
 template <int D, int KT>
@@ -687,28 +986,48 @@ hipError_t launch_kt(const FaArgs& a, int batch, int d, int nh, hipStream_t stre
 
 }  // namespace
 
-// Heads per work-group: the largest of 4, 2, 1 dividing the GQA group size.
-int fa_heads_per_wg(int hq, int hkv) {
-    const int group = hq / hkv;
-    for (int nh : {4, 2, 1})
-        if (nh <= P1X_FA_MAX_NH && group % nh == 0) return nh;
-    return 1;
-}
+#ifndef P1X_FA_MC_WGS
+#define P1X_FA_MC_WGS 256  // its pass-1 work-groups, at most (one per CU)
+#endif
+#ifndef P1X_FA_MC_MIN_KV
+#define P1X_FA_MC_MIN_KV 16384  // KV length from which the automatic choice is k_fa_mc
+#endif
 
-// KV split: chunks of whole work-group batches (kWaves waves x 64/(d/kDimsPerLane) groups x kKeys keys), about
-// P1X_FA_TARGET_WGS pass-1 work-groups in total, at most kMaxSplits splits.
-void fa_split_plan(int batch, int hq, int hkv, int seq_q, int seq_kv, int d, int& splits, int& chunk) {
-    const int kpb = kWaves * (64 / (d / kDimsPerLane)) * kKeys;
-    const int nh = fa_heads_per_wg(hq, hkv);
-    const long wgs_per_split = long(batch) * hkv * (hq / hkv / nh) * seq_q;
-    long want = (P1X_FA_TARGET_WGS + wgs_per_split - 1) / wgs_per_split;
+// Kernel selection of fa_plan: 0 automatic, 1 k_fa_split, 2 k_fa_mc wherever it applies (fp16 K/V, d 128).
+static std::atomic<int> g_fa_kernel{0};
+void fa_select_kernel(int kernel) { g_fa_kernel.store(kernel, std::memory_order_relaxed); }
+
+// The split plan: the kernel, heads per work-group (the largest of 4, 2, 1 dividing the GQA group that the kernel
+// supports), and chunks of whole work-group batches (64 keys at d 128) aiming at the kernel's target work-group
+// count, at most kMaxSplits splits. The automatic choice is k_fa_mc (fp16 K/V at d 128) from P1X_FA_MC_MIN_KV keys:
+// on gfx950 the two kernels cost about the same at 8192 keys (12.7 against 12.4 us for 32 query / 8 KV heads, both
+// passes), k_fa_mc is 10% faster at 32768 (28.7 against 31.7 us) and k_fa_split is faster below (7.4 against 8.5 us
+// at 2048). k_fa_mc rounds its split count down so that at most P1X_FA_MC_WGS work-groups, and so at most
+// 256 * 4 partial rows, are planned.
+FaPlan fa_plan(int batch, int hq, int hkv, int seq_q, int seq_kv, int d, bool kv_f16) {
+    FaPlan pl{};
+    const int sel = g_fa_kernel.load(std::memory_order_relaxed);
+    pl.mc = kv_f16 && d == 128 && (sel == 2 || (sel == 0 && seq_kv >= P1X_FA_MC_MIN_KV));
+    const int group = hq / hkv, max_nh = pl.mc ? 4 : P1X_FA_MAX_NH;
+    pl.nh = 1;
+    for (int nh : {4, 2})
+        if (nh <= max_nh && group % nh == 0) {
+            pl.nh = nh;
+            break;
+        }
+    pl.head_chunks = group / pl.nh;
+    const int kpb = pl.mc ? 16 * kMcWaves : kWaves * (64 / (d / kDimsPerLane)) * kKeys;
+    const long wgs_per_split = long(batch) * hkv * pl.head_chunks * seq_q;
+    const long target = pl.mc ? P1X_FA_MC_WGS : P1X_FA_TARGET_WGS;
+    long want = pl.mc ? target / wgs_per_split : (target + wgs_per_split - 1) / wgs_per_split;
     const long max_by_len = (seq_kv + kpb - 1) / kpb;
     want = want < 1 ? 1 : want;
     want = want > max_by_len ? max_by_len : want;
     want = want > kMaxSplits ? kMaxSplits : want;
-    chunk = int((seq_kv + want - 1) / want);
-    chunk = (chunk + kpb - 1) / kpb * kpb;
-    splits = (seq_kv + chunk - 1) / chunk;
+    pl.chunk = int((seq_kv + want - 1) / want);
+    pl.chunk = (pl.chunk + kpb - 1) / kpb * kpb;
+    pl.splits = (seq_kv + pl.chunk - 1) / pl.chunk;
+    return pl;
 }
 
 // Address of this device's `scratch`, looked up with hipGetSymbolAddress the first time each device asks (with
@@ -734,8 +1053,16 @@ hipError_t fa_scratch(void** out) {
 }
 
 hipError_t launch_fa_decode(FaArgs a, int batch, int d, hipStream_t stream) {
-    const int nh = fa_heads_per_wg(a.hq, a.hkv);
-    a.head_chunks = (a.hq / a.hkv) / nh;
+    const int nh = a.nh;
+    if (a.mc) {
+        if (a.kv_type != kKvF16 || d != 128) return hipErrorInvalidValue;
+        switch (nh) {
+            case 1: return launch_mc<1>(a, batch, stream);
+            case 2: return launch_mc<2>(a, batch, stream);
+            case 4: return launch_mc<4>(a, batch, stream);
+        }
+        return hipErrorInvalidValue;
+    }
     switch (a.kv_type) {
         case kKvF16: return launch_kt<kKvF16>(a, batch, d, nh, stream);
         case kKvQ8_0: return launch_kt<kKvQ8_0>(a, batch, d, nh, stream);

@@ -99,15 +99,22 @@ struct FaArgs {
     int64_t k_row, k_head, k_batch, v_row, v_head, v_batch;  // element strides
     uint32_t k_bytes, v_bytes;  // bytes spanned by one head's seq_kv rows of K and of V
     int hq, hkv, seq_q, seq_kv, causal, splits, chunk, head_chunks;
+    int nh, mc;  // query heads per pass-1 work-group; 1: the matrix-core pass (fp16 K/V, d 128)
     float scale, softcap;
 };
 hipError_t launch_fa_decode(FaArgs a, int batch, int d, hipStream_t stream);
+// Split plan of the decode attention for fp16 (kv_f16) or quantized K/V: kernel, heads per work-group, splits.
+struct FaPlan {
+    int nh, head_chunks, splits, chunk;
+    bool mc;
+};
+FaPlan fa_plan(int batch, int hq, int hkv, int seq_q, int seq_kv, int d, bool kv_f16);
+// The kernel fa_plan picks: 0 automatic (by KV length), 1 always k_fa_split, 2 k_fa_mc wherever it applies.
+void fa_select_kernel(int kernel);
 // Device scratch of the no-allocation attention entry point: a file-scope array of kFaScratchBytes in fattn.hip,
 // whose address on the current device fa_scratch() returns (looked up once per device).
 constexpr size_t kFaScratchBytes = size_t(1) << 20;
 hipError_t fa_scratch(void** out);
-int fa_heads_per_wg(int hq, int hkv);
-void fa_split_plan(int batch, int hq, int hkv, int seq_q, int seq_kv, int d, int& splits, int& chunk);
 
 // Decode-step glue (glue.hip). Device-resident state of a greedy decode: the position being decoded, the
 // prompt length, and the visible KV length of the current step (published by the embedding kernel).

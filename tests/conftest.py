@@ -43,5 +43,16 @@ def gpu():
     return lib
 
 
+@pytest.fixture(params=["split", "mc"])
+def fa_kernel(request, gpu):
+    """Runs an attention test once with each first-pass kernel forced (the vector pass, and the matrix-core pass
+    wherever it applies: fp16 K/V at d 128), then restores the automatic choice."""
+    import p100_amd as P
+
+    P.fa_select_kernel(request.param)
+    yield request.param
+    P.fa_select_kernel("auto")
+
+
 GOLDEN = ROOT / "tests" / "golden"
 os.environ.setdefault("OMP_NUM_THREADS", str(min(8, os.cpu_count() or 1)))

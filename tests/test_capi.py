@@ -143,3 +143,44 @@ def test_should_use_mmvh_and_overrides():
     assert _predicate_in_subprocess({"P1X_DISABLE_MMVH": "1"}) == [0, 0, 0, 0, 0]
     assert _predicate_in_subprocess({"P1X_FORCE_MMVH": "1"}) == [1, 1, 1, 0, 0]
     assert _predicate_in_subprocess({"P1X_FORCE_MMVH": "1", "P1X_DISABLE_MMVH": "1"}) == [1, 1, 1, 0, 0]
+
+
+def test_fa_kernel_selection_and_plan_bounds_without_gpu():
+    """The first-pass selection is host state: invalid values are refused; the automatic choice takes the
+    matrix-core pass (4 heads per work-group, at most 256 work-groups) from 16384 keys at d 128 and the vector pass
+    below; every d <= 128 plan of either kernel keeps its partials within 0.55 MiB (the no-allocation entry point's
+    documented bound)."""
+    import ctypes as C
+    import itertools
+
+    import p100_amd
+    import oracle
+
+    syms = p100_amd.load_symbols_only()
+    sel = syms["p1x_fa_select_kernel"]
+    sel.restype, sel.argtypes = C.c_int, [C.c_int]
+    ws = syms["p1x_flash_attn_decode_workspace"]
+    ws.restype, ws.argtypes = C.c_size_t, [C.c_void_p]
+
+    def need(**kw):
+        return ws(C.byref(p100_amd._params(oracle.AttnParams(**kw))))
+
+    cfg = dict(n_head_q=32, n_head_kv=8, seq_q=1, d_qk=128, d_v=128, causal=True)
+    try:
+        assert sel(3) == p100_amd.EINVAL and sel(-1) == p100_amd.EINVAL
+        assert sel(2) == p100_amd.OK
+        mc = {n: need(seq_kv=n, **cfg) for n in (8192, 32768)}
+        assert mc[32768] == 32 * 32 * 130 * 4  # 8 KV heads x 32 splits = 256 work-groups of 4 query heads
+        assert sel(1) == p100_amd.OK
+        split = {n: need(seq_kv=n, **cfg) for n in (8192, 32768)}
+        assert split[32768] != mc[32768]
+        assert sel(0) == p100_amd.OK
+        assert need(seq_kv=8192, **cfg) == split[8192] and need(seq_kv=32768, **cfg) == mc[32768]
+        for kernel in (1, 2):
+            assert sel(kernel) == p100_amd.OK
+            for b, hkv, grp, sq, skv, d in itertools.product((1, 2, 3), (1, 4, 7, 8, 32), (1, 2, 4, 8), (1, 3),
+                                                            (100, 4096, 40000), (64, 128)):
+                n = need(batch=b, n_head_q=hkv * grp, n_head_kv=hkv, seq_q=sq, seq_kv=skv, d_qk=d, d_v=d)
+                assert n <= 0.55 * (1 << 20), (kernel, b, hkv, grp, sq, skv, d, n)
+    finally:
+        sel(0)

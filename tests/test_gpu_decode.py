@@ -15,7 +15,7 @@ import pytest
 
 import p100_amd as P
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("fa_kernel")]
 
 
 def to_dev(a):

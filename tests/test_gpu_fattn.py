@@ -14,7 +14,7 @@ import math
 import numpy as np
 import pytest
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("fa_kernel")]
 
 INF = math.inf
 
