@@ -221,9 +221,9 @@ int p1x_flash_attn_decode_quant(const p1x_attn_params* p, int kv_type, const flo
                                 float* lse, void* ws, size_t ws_bytes, void* stream);
 
 /* Which first-pass kernel the decode attention plans with, for the whole process: P1X_FA_KERNEL_AUTO (the
- * default) takes the matrix-core pass for fp16 K/V with d_qk = 128 from 16384 keys and the vector pass otherwise;
- * _SPLIT always the vector pass; _MC the matrix-core pass wherever it applies (fp16 K/V, d_qk = 128). Both give
- * the same results within the FP32 accumulation tolerance; the choice changes the split plan, so query
+ * default) and _SPLIT take the vector pass; _MC the matrix-core pass (Q.K^T on fp16 MFMA) wherever it applies
+ * (fp16 K/V, d_qk = 128), an alternative measured against the vector pass and never chosen automatically. Both
+ * give the same results within the FP32 accumulation tolerance; the choice changes the split plan, so query
  * p1x_flash_attn_decode_workspace after changing it. No counterpart in the reference (ggml picks its FA kernel
  * per device and shape, fattn.cu:541-719); for tuning and for testing both kernels. */
 enum { P1X_FA_KERNEL_AUTO = 0, P1X_FA_KERNEL_SPLIT = 1, P1X_FA_KERNEL_MC = 2 };

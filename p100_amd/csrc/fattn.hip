@@ -989,25 +989,21 @@ hipError_t launch_kt(const FaArgs& a, int batch, int d, int nh, hipStream_t stre
 #ifndef P1X_FA_MC_WGS
 #define P1X_FA_MC_WGS 256  // its pass-1 work-groups, at most (one per CU)
 #endif
-#ifndef P1X_FA_MC_MIN_KV
-#define P1X_FA_MC_MIN_KV 16384  // KV length from which the automatic choice is k_fa_mc
-#endif
-
-// Kernel selection of fa_plan: 0 automatic, 1 k_fa_split, 2 k_fa_mc wherever it applies (fp16 K/V, d 128).
+// Kernel selection of fa_plan: 0 automatic (k_fa_split), 1 k_fa_split, 2 k_fa_mc wherever it applies (fp16 K/V,
+// d 128).
 static std::atomic<int> g_fa_kernel{0};
 void fa_select_kernel(int kernel) { g_fa_kernel.store(kernel, std::memory_order_relaxed); }
 
 // The split plan: the kernel, heads per work-group (the largest of 4, 2, 1 dividing the GQA group that the kernel
 // supports), and chunks of whole work-group batches (64 keys at d 128) aiming at the kernel's target work-group
-// count, at most kMaxSplits splits. The automatic choice is k_fa_mc (fp16 K/V at d 128) from P1X_FA_MC_MIN_KV keys:
-// on gfx950 the two kernels cost about the same at 8192 keys (12.7 against 12.4 us for 32 query / 8 KV heads, both
-// passes), k_fa_mc is 10% faster at 32768 (28.7 against 31.7 us) and k_fa_split is faster below (7.4 against 8.5 us
-// at 2048). k_fa_mc rounds its split count down so that at most P1X_FA_MC_WGS work-groups, and so at most
-// 256 * 4 partial rows, are planned.
+// count, at most kMaxSplits splits. The automatic choice is always the vector pass k_fa_split: decode attention is
+// not a dense contraction, and on gfx950 the matrix-core pass gains nothing where decode spends its time (12.7
+// against 12.4 us at 8192 keys for 32 query / 8 KV heads, both passes; 8.5 against 7.4 us at 2048), only 10% at
+// 32768 keys (28.7 against 31.7 us). k_fa_mc, when selected, rounds its split count down so that at most
+// P1X_FA_MC_WGS work-groups, and so at most 256 * 4 partial rows, are planned.
 FaPlan fa_plan(int batch, int hq, int hkv, int seq_q, int seq_kv, int d, bool kv_f16) {
     FaPlan pl{};
-    const int sel = g_fa_kernel.load(std::memory_order_relaxed);
-    pl.mc = kv_f16 && d == 128 && (sel == 2 || (sel == 0 && seq_kv >= P1X_FA_MC_MIN_KV));
+    pl.mc = kv_f16 && d == 128 && g_fa_kernel.load(std::memory_order_relaxed) == 2;
     const int group = hq / hkv, max_nh = pl.mc ? 4 : P1X_FA_MAX_NH;
     pl.nh = 1;
     for (int nh : {4, 2})

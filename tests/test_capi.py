@@ -146,9 +146,9 @@ def test_should_use_mmvh_and_overrides():
 
 
 def test_fa_kernel_selection_and_plan_bounds_without_gpu():
-    """The first-pass selection is host state: invalid values are refused; the automatic choice takes the
-    matrix-core pass (4 heads per work-group, at most 256 work-groups) from 16384 keys at d 128 and the vector pass
-    below; every d <= 128 plan of either kernel keeps its partials within 0.55 MiB (the no-allocation entry point's
+    """The first-pass selection is host state: invalid values are refused; the automatic choice is the vector
+    pass at every length, the forced matrix-core pass plans 4 heads per work-group and at most 256 work-groups;
+    every d <= 128 plan of either kernel keeps its partials within 0.55 MiB (the no-allocation entry point's
     documented bound)."""
     import ctypes as C
     import itertools
@@ -175,7 +175,7 @@ def test_fa_kernel_selection_and_plan_bounds_without_gpu():
         split = {n: need(seq_kv=n, **cfg) for n in (8192, 32768)}
         assert split[32768] != mc[32768]
         assert sel(0) == p100_amd.OK
-        assert need(seq_kv=8192, **cfg) == split[8192] and need(seq_kv=32768, **cfg) == mc[32768]
+        assert need(seq_kv=8192, **cfg) == split[8192] and need(seq_kv=32768, **cfg) == split[32768]
         for kernel in (1, 2):
             assert sel(kernel) == p100_amd.OK
             for b, hkv, grp, sq, skv, d in itertools.product((1, 2, 3), (1, 4, 7, 8, 32), (1, 2, 4, 8), (1, 3),
