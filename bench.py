@@ -108,8 +108,13 @@ def main():
                          "picks one shape), 'read' = the read-ceiling probe, 'mmvh' = the h16 kernels")
     ap.add_argument("--kquant", default=None, help="with --only kquant: one of q4_K:14336x4096, q4_K:4096x14336, "
                                                      "q6_K:128256x4096")
+    ap.add_argument("--mmvh", default=None, help="with --only mmvh: one TYPE:MxK of the h16 comparison (e.g. "
+                                                   "q4_K:4096x14336)")
     ap.add_argument("--cols", type=int, nargs="+", default=[4, 16])
     ap.add_argument("--fa-ctx", type=int, nargs="+", default=[512, 640, 2048, 8192, 32768])
+    ap.add_argument("--fa-kernel", choices=("auto", "split", "mc"), default="auto",
+                    help="first-pass attention kernel (p1x_fa_select_kernel): the automatic choice, the vector "
+                         "pass, or the matrix-core alternative")
     ap.add_argument("--fa-fp16-only", action="store_true",
                     help="with --only fa: the fp16 cache at --fa-ctx alone (no device-length or quantized-cache "
                          "runs), so a profile of the run holds one configuration")
@@ -125,6 +130,7 @@ def main():
     from p100_amd import synth
 
     lib = P.load()
+    P.fa_select_kernel(args.fa_kernel)
     dev = torch.device("cuda")
     if args.only == "decode":
         print(json.dumps({"only": "decode", "decode_8b": measure_decode(torch)}))
@@ -163,7 +169,7 @@ def main():
             print(json.dumps({"only": "kquant", "kquant": measure_kquant(torch, P, lib, synth, timer, gen,
                                                                          args.kquant)}))
         else:
-            print(json.dumps({"only": "mmvh", "mmvh": measure_mmvh(torch, P, lib, synth, timer, gen)}))
+            print(json.dumps({"only": "mmvh", "mmvh": measure_mmvh(torch, P, lib, synth, timer, gen, args.mmvh)}))
         return
     log(f"[bench] {torch.cuda.get_device_name(0)}; building {args.layers} Q4_0 layers")
     gen = torch.Generator(device="cuda")
@@ -490,20 +496,25 @@ def measure_kquant(torch, P, lib, synth, timer, gen, only=None):
 MMVH_SHAPES = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]
 
 
-def measure_mmvh(torch, P, lib, synth, timer, gen):
+def measure_mmvh(torch, P, lib, synth, timer, gen, only=None):
     """The h16 (MMVH) mat-vec kernel against the Q8_1 (MMVQ) kernel on prepared activations, at the Llama-3-8B
-    layer shapes, ne11 in {1, 4, 8}: the measurements behind p1x_should_use_mmvh."""
+    layer shapes, ne11 in {1, 4, 8}: the measurements behind p1x_should_use_mmvh. only = "TYPE:MxK" keeps one."""
     out = {}
     for tname in ("q4_0", "q8_0", "q4_K", "q6_K"):
         t = P.TYPES[tname]
         for M, K in MMVH_SHAPES:
+            if only is not None and only != f"{tname}:{M}x{K}":
+                continue
             for n in (1, 4, 8):
                 h = measure_matvec(torch, P, lib, synth, timer, gen, t, M, K, n, act="h16", prepared=True)
                 q = measure_matvec(torch, P, lib, synth, timer, gen, t, M, K, n, act="q8_1", prepared=True)
                 out[f"{tname} {M}x{K} n={n}"] = {"h16_us": h["us"], "q8_1_us": q["us"], "h16_gbs": h["gbs"],
                                                   "q8_1_gbs": q["gbs"]}
-        log(f"[bench] mmvh {tname}: " + ", ".join(f"{k.split(' ', 1)[1]} h16 {v['h16_us']} / q8_1 {v['q8_1_us']} us"
-                                                for k, v in out.items() if k.startswith(tname)))
+        if any(k.startswith(tname) for k in out):
+            log(f"[bench] mmvh {tname}: " + ", ".join(f"{k.split(' ', 1)[1]} h16 {v['h16_us']} / q8_1 {v['q8_1_us']} us"
+                                                    for k, v in out.items() if k.startswith(tname)))
+    if only is not None and not out:
+        raise SystemExit(f"--mmvh {only}: not one of the measured TYPE:MxK")
     return out
 
 
