@@ -13,9 +13,11 @@
 // 4 (l / 16) .. + 3 of column l % 16. A = weights, B = activation, so a lane's four results share its own
 // activation column (one scale load) and need the weight scales of four rows (read from the staged rows in LDS).
 //
-// Work-group: 16 weight rows, 8 waves (up to 8192 rows) or 4, each over a contiguous share of the K blocks, 8
-// blocks per step staged through the wave's own LDS area with the next step's loads in flight; the partial
+// Work-group: 16 weight rows, 8 waves (up to 8192 rows) or 4, each over a contiguous share of the K blocks, 16
+// (q4_0) or 8 (q8_0) blocks per step staged through the wave's own LDS area with the next step's loads in flight; the partial
 // 16 x 16 tiles are added in LDS in a fixed order (deterministic, no workspace). Grid: ceil(M / 16).
+#include <type_traits>
+
 #include "common.h"
 #include "launch.h"
 
@@ -51,7 +53,14 @@ struct MfmaW<Q8_0> {
 #ifndef P1X_MMQ_PAD
 #define P1X_MMQ_PAD 4
 #endif
-constexpr int kStepBlocks = 8;  // K blocks per step (staged through LDS)
+#ifndef P1X_MMQ_STEP_Q4_0
+#define P1X_MMQ_STEP_Q4_0 8  // K blocks per step (staged through LDS) for q4_0 (16: slower); q8_0 takes 8
+#endif
+template <int TYPE>
+constexpr int step_blocks() { return TYPE == Q4_0 ? P1X_MMQ_STEP_Q4_0 : 8; }
+#ifndef P1X_MMQ_UNROLL
+#define P1X_MMQ_UNROLL 8  // blocks of a step unrolled together (more keeps too many operands live)
+#endif
 
 // Buffer loads with a range check: offsets at or past the resource size read zeros and touch no memory, so the
 // staging loads past the matrix end, past the last activation column or in padded columns need no branch.
@@ -64,15 +73,16 @@ __device__ __forceinline__ uint4 ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 }
 constexpr uint32_t kOob = 0x7ffffff0u;
 
-// Per-wave LDS staging area of one step: the 16 weight rows' bytes of 8 blocks (dword-aligned spans, 4 lanes x NWL
-// 16-byte loads per row: 192 bytes for q4_0, 320 for q8_0, each covering 8 blocks plus the 2-byte alignment shift),
-// the 16 activation columns' 8 blocks as [block][column][32 bytes] (the MFMA B-operand reads are then 512
-// contiguous bytes per block), and their Q8_1 scales [block][column].
-template <int ROWDW>
+// Per-wave LDS staging area of one step of U blocks: the 16 weight rows' bytes (dword-aligned spans, 4 lanes x NWL
+// 16-byte loads per row: 320 bytes for 16 q4_0 blocks, 320 for 8 q8_0 blocks, each covering the step's blocks plus
+// the 2-byte alignment shift), the 16 activation columns' U blocks as [block][column][32 bytes] (the MFMA B-operand
+// reads are then 512 contiguous bytes per block), and their Q8_1 scales [block][column].
+template <int ROWDW, int U>
 struct MmqStage {
     uint32_t w[16][ROWDW];
-    uint32_t a[kStepBlocks][16][8];
-    float4 s[kStepBlocks][16];
+    uint32_t a[U][16][8];
+    float4 s[U][16];
+    float dw[U][16];  // the weight scales of the step, decoded once per (block, row)
 };
 
 // NW waves per work-group, each over a contiguous share of the K blocks: 8 where the grid is small (M <= 8192, at
@@ -83,11 +93,13 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
                                                             const float4* __restrict__ xds, float* __restrict__ y,
                                                             int32_t* __restrict__ gs) {
     using W = MfmaW<TYPE>;
-    constexpr int U = kStepBlocks;
+    constexpr int U = step_blocks<TYPE>();
+    static_assert(U == 8 || U == 16, "activation staging covers 8 or 16 blocks per step");
     constexpr int BB = W::kBytes;
     constexpr int NWL = (U * BB + 4 + 63) / 64;  // 16-byte loads per lane (4 lanes per row)
     constexpr int ROWDW = 16 * NWL + P1X_MMQ_PAD;  // staged dwords per row (padding spreads rows over LDS banks)
-    __shared__ MmqStage<ROWDW> stage[NW];
+    constexpr int NA = U / 2, NS = U / 4;  // activation and scale loads per lane (16 columns x U blocks)
+    __shared__ MmqStage<ROWDW, U> stage[NW];
     __shared__ float red[NW - 1][4][64];  // partial tiles of waves 1.., result-major (conflict-free)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, i16 = lane & 15;
@@ -95,7 +107,7 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
     const int nblk = K / 32;
     const int per = (nblk + NW - 1) / NW;
     const int b0 = min(nblk, wave * per), b1 = min(nblk, b0 + per);
-    MmqStage<ROWDW>& st = stage[wave];
+    MmqStage<ROWDW, U>& st = stage[wave];
 
     // Global side of the staging: lane (row lane/4, quarter lane%4) reads NWL x 16 bytes of its row's dword-aligned
     // span.
@@ -110,34 +122,34 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
     // MFMA side: the lane's A-operand row (i16) and the rows 4g..4g+3 whose scales it applies; byte 0 of each
     // row's staged span is the dword holding the row's first byte of the step.
     auto row_shift = [&](int row, int bs) { return int((size_t(min(m0 + row, M - 1)) * nb01 + size_t(bs) * BB) & 3); };
-    uint4 rw[NWL], ra[4], rs[2];
+    uint4 rw[NWL], ra[NA], rs[NS];
     auto load = [&](int bs) {
         const uint32_t wb = (srow_off + uint32_t(bs) * BB) & ~3u;
 #pragma unroll
         for (int k = 0; k < NWL; ++k) rw[k] = ld16(wr, wb + (sq * NWL + k) * 16);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {  // piece p: column p / 16, 16-byte piece p % 16 of the column's 256 bytes
-            const int p = j * 64 + lane, c = p >> 4;
-            ra[j] = ld16(xr, c < B ? uint32_t(c * K + bs * 32 + (p & 15) * 16) : kOob);
+        for (int j = 0; j < NA; ++j) {  // piece p: column p / 2U, 16-byte piece p % 2U of the column's 32U bytes
+            const int p = j * 64 + lane, c = p / (2 * U);
+            ra[j] = ld16(xr, c < B ? uint32_t(c * K + bs * 32 + (p % (2 * U)) * 16) : kOob);
         }
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {  // piece p: column p / 8, block p % 8
-            const int p = j * 64 + lane, c = p >> 3;
-            rs[j] = ld16(dr, c < B ? uint32_t((c * nblk + bs + (p & 7)) * 16) : kOob);
+        for (int j = 0; j < NS; ++j) {  // piece p: column p / U, block p % U
+            const int p = j * 64 + lane, c = p / U;
+            rs[j] = ld16(dr, c < B ? uint32_t((c * nblk + bs + p % U) * 16) : kOob);
         }
     };
     auto store = [&]() {
 #pragma unroll
         for (int k = 0; k < NWL; ++k) *reinterpret_cast<uint4*>(&st.w[srow][(sq * NWL + k) * 4]) = rw[k];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int p = j * 64 + lane, c = p >> 4, k16 = p & 15;
+        for (int j = 0; j < NA; ++j) {
+            const int p = j * 64 + lane, c = p / (2 * U), k16 = p % (2 * U);
             *reinterpret_cast<uint4*>(&st.a[k16 >> 1][c][(k16 & 1) * 4]) = ra[j];
         }
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < NS; ++j) {
             const int p = j * 64 + lane;
-            st.s[p & 7][p >> 3] = __builtin_bit_cast(float4, rs[j]);
+            st.s[p % U][p / U] = __builtin_bit_cast(float4, rs[j]);
         }
     };
     // 16-bit field at byte offset o of staged row r.
@@ -150,6 +162,39 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
     };
 
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // Block u of a step: the MFMA of row tile x column tile, then each lane's four (row, column) sums scaled into
+    // its accumulators. kTail: the last step of a share shorter than U blocks (the blocks past b1 are skipped).
+    auto block = [&](int bs, int u, int sh, auto tail_tag) {
+        constexpr bool kTail = decltype(tail_tag)::value;
+        const bool ok = !kTail || bs + u < b1;
+        // A operand: 8 weight elements 8g..8g+7 of block u of row i16.
+        long wa;
+        if constexpr (TYPE == Q4_0) {
+            uint32_t q2[2];
+            bytes_at(i16, sh + u * BB + 2 + 8 * (g & 1), q2, 2);
+            const uint32_t shn = (g & 2) ? 4u : 0u;
+            wa = long((q2[0] >> shn) & 0x0F0F0F0Fu) | (long((q2[1] >> shn) & 0x0F0F0F0Fu) << 32);
+        } else {
+            uint32_t q2[2];
+            bytes_at(i16, sh + u * BB + 2 + 8 * g, q2, 2);
+            wa = long(q2[0]) | (long(q2[1]) << 32);
+        }
+        const long xa = *reinterpret_cast<const long*>(&st.a[u][i16][2 * g]);
+        const float4 xs = st.s[u][i16];
+        const v4i zero = {0, 0, 0, 0};
+        const v4i dd = __builtin_amdgcn_mfma_i32_16x16x32_i8(wa, xa, zero, 0, 0, 0);
+        const float4 dw4 = *reinterpret_cast<const float4*>(&st.dw[u][4 * g]);
+        const float dw[4] = {dw4.x, dw4.y, dw4.z, dw4.w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float v = W::acc(dw[r], dd[r], xs, acc[r]);
+            acc[r] = ok ? v : acc[r];
+            if (SUMS) {
+                const int m = m0 + 4 * g + r;
+                if (ok && i16 < B && m < M) gs[(size_t(i16) * M + m) * nblk + bs + u] = dd[r];
+            }
+        }
+    };
     if (b0 < b1) {
         load(b0);
         for (int bs = b0; bs < b1; bs += U) {
@@ -162,40 +207,23 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            // The step's weight scales, decoded once: lane (row lane % 16, blocks lane / 16 + 4 k).
+#pragma unroll
+            for (int k = 0; k < U / 4; ++k) {
+                const int row = lane & 15, u = (lane >> 4) + 4 * k;
+                st.dw[u][row] = half_bits_to_float(u16_at(row, row_shift(row, bs) + u * BB));
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             load(bs + U);  // the next step's loads are in flight while this one computes (past b1: never used)
             const int sh = row_shift(i16, bs);
-            int shr[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) shr[r] = row_shift(4 * g + r, bs);
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const bool ok = bs + u < b1;
-                // A operand: 8 weight elements 8g..8g+7 of block u of row i16.
-                long wa;
-                if constexpr (TYPE == Q4_0) {
-                    uint32_t q2[2];
-                    bytes_at(i16, sh + u * BB + 2 + 8 * (g & 1), q2, 2);
-                    const uint32_t shn = (g & 2) ? 4u : 0u;
-                    wa = long((q2[0] >> shn) & 0x0F0F0F0Fu) | (long((q2[1] >> shn) & 0x0F0F0F0Fu) << 32);
-                } else {
-                    uint32_t q2[2];
-                    bytes_at(i16, sh + u * BB + 2 + 8 * g, q2, 2);
-                    wa = long(q2[0]) | (long(q2[1]) << 32);
-                }
-                const long xa = *reinterpret_cast<const long*>(&st.a[u][i16][2 * g]);
-                const float4 xs = st.s[u][i16];
-                const v4i zero = {0, 0, 0, 0};
-                const v4i dd = __builtin_amdgcn_mfma_i32_16x16x32_i8(wa, xa, zero, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float dw = half_bits_to_float(u16_at(4 * g + r, shr[r] + u * BB));
-                    const float v = W::acc(dw, dd[r], xs, acc[r]);
-                    acc[r] = ok ? v : acc[r];
-                    if (SUMS) {
-                        const int m = m0 + 4 * g + r;
-                        if (ok && i16 < B && m < M) gs[(size_t(i16) * M + m) * nblk + bs + u] = dd[r];
-                    }
-                }
+            if (bs + U <= b1) {
+#pragma unroll P1X_MMQ_UNROLL
+                for (int u = 0; u < U; ++u) block(bs, u, sh, std::false_type{});
+            } else {
+#pragma unroll P1X_MMQ_UNROLL
+                for (int u = 0; u < U; ++u) block(bs, u, sh, std::true_type{});
             }
         }
     }

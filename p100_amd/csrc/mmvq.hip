@@ -43,6 +43,12 @@
 #ifndef P1X_MMVQ_MAX_RW
 #define P1X_MMVQ_MAX_RW 4
 #endif
+#ifndef P1X_MMVR_ROWS_LONG
+#define P1X_MMVR_ROWS_LONG 4  // k_mmvr rows per row-group for rows of 257..512 units
+#endif
+#ifndef P1X_MMVR_NWK_LONG
+#define P1X_MMVR_NWK_LONG 4  // and waves per row (units per thread: 512 / (64 * waves))
+#endif
 #ifndef P1X_MMVR_ENABLE
 #define P1X_MMVR_ENABLE 1  // one prepared q4_0 / q8_0 column: register-resident activation kernel (k_mmvr)
 #endif
@@ -756,7 +762,7 @@ bool mmvr_plan(int type, int M, int K, MmvrPlan& p) {
     } else if (units <= 256) {
         p = {2, 2, 2};
     } else if (units <= 512) {
-        p = {4, 2, 4};
+        p = {P1X_MMVR_NWK_LONG, 8 / P1X_MMVR_NWK_LONG, P1X_MMVR_ROWS_LONG};
     } else {
         return false;
     }
@@ -797,7 +803,9 @@ hipError_t launch_mmvr(const MmvrPlan& p, const uint8_t* w, int64_t nb01, int M,
         P1X_MMVR(2, 1, 2)
         P1X_MMVR(2, 1, 4)
         P1X_MMVR(2, 2, 2)
-        P1X_MMVR(4, 2, 4)
+        if constexpr (!EPI::kPairs || P1X_MMVR_ROWS_LONG % 2 == 0) {
+            P1X_MMVR(P1X_MMVR_NWK_LONG, 8 / P1X_MMVR_NWK_LONG, P1X_MMVR_ROWS_LONG)
+        }
     }
 #undef P1X_MMVR
     return hipErrorInvalidValue;
