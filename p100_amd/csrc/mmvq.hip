@@ -1017,6 +1017,14 @@ int mmvq_rows_per_wave(int M, int B, bool fused) {
     return 1;
 }
 
+// The streaming kernel's rows per wave for a weight type: one for K-quant rows at one column, whose units hold about
+// 20 registers each (with 4 rows a wave held 277 VGPRs, one wave per SIMD; on 128256x4096 Q6_K one row per wave
+// takes 105.4 us against 178.6, on 14336x4096 Q4_K 9.02 against 9.32), else mmvq_rows_per_wave.
+int mmvq_type_rows_per_wave(int type, int M, int B, bool fused) {
+    if ((type == Q4_K || type == Q6_K) && B == 1 && !fused) return 1;
+    return mmvq_rows_per_wave(M, B, fused);
+}
+
 // The single-launch form (x quantized into LDS by each work-group), for one column, when its 48 bytes per block
 // fit in 64 KiB of LDS and the repeated quantization (work-groups x K elements) stays small next to the weight
 // stream; otherwise the activation goes through p1x_quantize_q8_1 and a workspace.
@@ -1029,7 +1037,7 @@ bool mmvq_fused_fits(int B, int M, int K) {
 
 hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
                        const float* x, float* y, int32_t* gs, hipStream_t stream) {
-    const int rw = mmvq_rows_per_wave(M, B, x != nullptr);
+    const int rw = mmvq_type_rows_per_wave(type, M, B, x != nullptr);
     const auto* wb = static_cast<const uint8_t*>(w);
     const auto* d4 = reinterpret_cast<const float4*>(xds);
     MmvrPlan plan;
@@ -1050,7 +1058,7 @@ hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int 
 
 hipError_t launch_mmvq_batched(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq,
                                const float* xds, float* y, const Slices& sl, hipStream_t stream) {
-    const int rw = mmvq_rows_per_wave(M, B, false);
+    const int rw = mmvq_type_rows_per_wave(type, M, B, false);
     const auto* wb = static_cast<const uint8_t*>(w);
     const auto* d4 = reinterpret_cast<const float4*>(xds);
     switch (type) {
