@@ -38,6 +38,8 @@
  *                            for callers that cannot allocate)
  *   p1x_flash_attn_decode_quant  the same op over a q8_0 / q4_0 KV cache, replacing the F16 conversion kernels that
  *                            ggml runs first (third_party/patches/0001, 0002; bench/micro/dequant_nc.cu:1-14)
+ *   p1x_fa_select_kernel     the first-pass kernel of the attention plan (no counterpart in the reference, which
+ *                            picks its FA kernel per device and shape in fattn.cu:541-719; a tuning and test hook)
  * Decode-step glue and driver (the llama-bench decode runs, bench/phase0.sh:124, of the 8B shape modelled in
  * bin/decode-model.py:52-57; the ggml ops are restated from llama.cpp's Llama graph, not from this reference):
  *   p1x_get_rows             GGML_OP_GET_ROWS (token embedding), q4_0 / q8_0 rows
