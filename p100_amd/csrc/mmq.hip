@@ -77,17 +77,19 @@ constexpr uint32_t kOob = 0x7ffffff0u;
 // 16-byte loads per row: 320 bytes for 16 q4_0 blocks, 320 for 8 q8_0 blocks, each covering the step's blocks plus
 // the 2-byte alignment shift), the 16 activation columns' U blocks as [block][column][32 bytes] (the MFMA B-operand
 // reads are then 512 contiguous bytes per block), and their Q8_1 scales [block][column].
-template <int ROWDW, int U>
+template <int ROWDW, int U, int BC>
 struct MmqStage {
     uint32_t w[16][ROWDW];
-    uint32_t a[U][16][8];
-    float4 s[U][16];
+    uint32_t a[U][BC][8];
+    float4 s[U][BC];
     float dw[U][16];  // the weight scales of the step, decoded once per (block, row)
 };
 
 // NW waves per work-group, each over a contiguous share of the K blocks: 8 where the grid is small (M <= 8192, at
 // most 512 work-groups, so a CU holds one and 8 waves give each SIMD two), 4 above (more work-groups per CU).
-template <int TYPE, bool SUMS, int NW>
+// BC: activation columns staged (16; or 8 when at most 8 are used, which halves the activation staging so that
+// more waves fit a CU's LDS; the B operand's columns 8..15 then read columns 0..7 again and their sums are dropped).
+template <int TYPE, bool SUMS, int NW, int BC>
 __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict__ w, int64_t nb01, int M, int K,
                                                             int B, const int8_t* __restrict__ xq,
                                                             const float4* __restrict__ xds, float* __restrict__ y,
@@ -98,8 +100,9 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
     constexpr int BB = W::kBytes;
     constexpr int NWL = (U * BB + 4 + 63) / 64;  // 16-byte loads per lane (4 lanes per row)
     constexpr int ROWDW = 16 * NWL + P1X_MMQ_PAD;  // staged dwords per row (padding spreads rows over LDS banks)
-    constexpr int NA = U / 2, NS = U / 4;  // activation and scale loads per lane (16 columns x U blocks)
-    __shared__ MmqStage<ROWDW, U> stage[NW];
+    static_assert(BC == 8 || BC == 16, "8 or 16 staged columns");
+    constexpr int NA = U * BC / 32, NS = U * BC / 64;  // activation and scale loads per lane (BC columns x U blocks)
+    __shared__ MmqStage<ROWDW, U, BC> stage[NW];
     __shared__ float red[NW - 1][4][64];  // partial tiles of waves 1.., result-major (conflict-free)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, i16 = lane & 15;
@@ -107,7 +110,7 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
     const int nblk = K / 32;
     const int per = (nblk + NW - 1) / NW;
     const int b0 = min(nblk, wave * per), b1 = min(nblk, b0 + per);
-    MmqStage<ROWDW, U>& st = stage[wave];
+    MmqStage<ROWDW, U, BC>& st = stage[wave];
 
     // Global side of the staging: lane (row lane/4, quarter lane%4) reads NWL x 16 bytes of its row's dword-aligned
     // span.
@@ -179,8 +182,8 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
             bytes_at(i16, sh + u * BB + 2 + 8 * g, q2, 2);
             wa = long(q2[0]) | (long(q2[1]) << 32);
         }
-        const long xa = *reinterpret_cast<const long*>(&st.a[u][i16][2 * g]);
-        const float4 xs = st.s[u][i16];
+        const long xa = *reinterpret_cast<const long*>(&st.a[u][i16 % BC][2 * g]);
+        const float4 xs = st.s[u][i16 % BC];
         const v4i zero = {0, 0, 0, 0};
         const v4i dd = __builtin_amdgcn_mfma_i32_16x16x32_i8(wa, xa, zero, 0, 0, 0);
         const float4 dw4 = *reinterpret_cast<const float4*>(&st.dw[u][4 * g]);
@@ -248,6 +251,16 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
 
 }  // namespace
 
+#ifndef P1X_MMQ_NW_NARROW
+#define P1X_MMQ_NW_NARROW 8  // waves per work-group at <= 8 columns on <= 8192 rows (8 staged columns)
+#endif
+
+#ifndef P1X_MMQ_MIN_COLS_LONG_Q4_0
+#define P1X_MMQ_MIN_COLS_LONG_Q4_0 5  // columns from which rows longer than 8192 take the matrix-core form (q4_0)
+#endif
+#ifndef P1X_MMQ_MIN_COLS_LONG_Q8_0
+#define P1X_MMQ_MIN_COLS_LONG_Q8_0 5  // (q8_0)
+#endif
 #ifndef P1X_MMQ_MIN_COLS
 #define P1X_MMQ_MIN_COLS 9  // columns from which the matrix-core form replaces the dot4 kernels
 #endif
@@ -258,15 +271,15 @@ bool mmq_fits(int M, int64_t nb01, int K, int B) {
     return int64_t(M) * nb01 + 3 <= int64_t(kOob) && int64_t(B) * K <= int64_t(kOob) &&
            int64_t(B) * (K / 32) * 16 <= int64_t(kOob);
 }
-// From 9 columns always; also rows longer than 8192 on at most 8192 rows (the 8-wave form) from 5 columns for q8_0
-// and 7 for q4_0, where the dot4 kernel's LDS-staged activation (B x 14336 x 1.5 bytes per work-group) outweighs
-// it (4096x14336, graph period, dot4 at 5 / 6 / 7 / 8 columns against the matrix-core form at any count: q8_0
-// 30.4 / 33.8 / 36.1 / 43.2 against 25.9 us; q4_0 20.3 / 23.2 / 26.8 / 29.5 against 22.6 us). K <= 8192 stays on
-// dot4 up to 8 columns (e.g. 4096x4096 at 8 columns 8.5 against 9.5 us).
+// From 9 columns always; also rows longer than 8192 on at most 8192 rows (the 8-wave form) from 5 columns, where
+// the dot4 kernel's LDS-staged activation (B x 14336 x 1.5 bytes per work-group) outweighs it (4096x14336, graph
+// period, dot4 against the 8-column-staging matrix-core form at 4 / 5 / 6 / 7 / 8 columns: q4_0 15.0 / 24.3 / 27.0
+// (dot4) against 17.4 / 16.9 / 17.0 / 17.2 / 17.2 us; q8_0 18.9 (dot4, 4 columns) against 20.7 / 21.0 / 21.3 /
+// 21.5 / 21.7 us). K <= 8192 stays on dot4 up to 8 columns (e.g. 4096x4096 at 8 columns 8.5 against 9.5 us).
 bool mmq_preferred(int type, int B, int M, int K) {
     if (!mmq_supported(type, B)) return false;
     if (B >= P1X_MMQ_MIN_COLS) return true;
-    return K > 8192 && M <= 8192 && B >= (type == Q8_0 ? 5 : 7);
+    return K > 8192 && M <= 8192 && B >= (type == Q8_0 ? P1X_MMQ_MIN_COLS_LONG_Q8_0 : P1X_MMQ_MIN_COLS_LONG_Q4_0);
 }
 
 hipError_t launch_mmq(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
@@ -276,10 +289,13 @@ hipError_t launch_mmq(int type, int B, const void* w, int64_t nb01, int M, int K
     const auto* d4 = reinterpret_cast<const float4*>(xds);
 #define P1X_MMQ(T, S) \
     do {                                                                                                           \
-        if (M <= 8192)                                                                                             \
-            hipLaunchKernelGGL((k_mmq_mfma<T, S, 8>), grid, dim3(512), 0, stream, wb, nb01, M, K, B, xq, d4, y, gs); \
+        if (B <= 8 && M <= 8192)                                                                                   \
+            hipLaunchKernelGGL((k_mmq_mfma<T, S, P1X_MMQ_NW_NARROW, 8>), grid, dim3(64 * P1X_MMQ_NW_NARROW), 0,     \
+                               stream, wb, nb01, M, K, B, xq, d4, y, gs);                                        \
+        else if (M <= 8192)                                                                                        \
+            hipLaunchKernelGGL((k_mmq_mfma<T, S, 8, 16>), grid, dim3(512), 0, stream, wb, nb01, M, K, B, xq, d4, y, gs); \
         else                                                                                                       \
-            hipLaunchKernelGGL((k_mmq_mfma<T, S, 4>), grid, dim3(256), 0, stream, wb, nb01, M, K, B, xq, d4, y, gs); \
+            hipLaunchKernelGGL((k_mmq_mfma<T, S, 4, 16>), grid, dim3(256), 0, stream, wb, nb01, M, K, B, xq, d4, y, gs); \
     } while (0)
     if (type == Q4_0) {
         if (gs) P1X_MMQ(Q4_0, true);

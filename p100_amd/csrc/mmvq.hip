@@ -43,6 +43,9 @@
 #ifndef P1X_MMVQ_MAX_RW
 #define P1X_MMVQ_MAX_RW 4
 #endif
+#ifndef P1X_MMVQ_KQ_RW1_COLS
+#define P1X_MMVQ_KQ_RW1_COLS 1  // K-quant column counts that take one row per wave
+#endif
 #ifndef P1X_MMVR_ROWS_LONG
 #define P1X_MMVR_ROWS_LONG 4  // k_mmvr rows per row-group for rows of 257..512 units
 #endif
@@ -1021,7 +1024,7 @@ int mmvq_rows_per_wave(int M, int B, bool fused) {
 // 20 registers each (with 4 rows a wave held 277 VGPRs, one wave per SIMD; on 128256x4096 Q6_K one row per wave
 // takes 105.4 us against 178.6, on 14336x4096 Q4_K 9.02 against 9.32), else mmvq_rows_per_wave.
 int mmvq_type_rows_per_wave(int type, int M, int B, bool fused) {
-    if ((type == Q4_K || type == Q6_K) && B == 1 && !fused) return 1;
+    if ((type == Q4_K || type == Q6_K) && B <= P1X_MMVQ_KQ_RW1_COLS && !fused) return 1;
     return mmvq_rows_per_wave(M, B, fused);
 }
 

@@ -179,8 +179,8 @@ def test_many_columns_parity(orc, gpu, tname):
 
 @pytest.mark.parametrize("tname", ["q4_0", "q8_0"])
 def test_long_rows_five_to_eight_columns(orc, gpu, tname):
-    """Rows longer than 8192 at 5-8 columns (the matrix-core form from 5 columns for q8_0 and 7 for q4_0, dot4
-    below): sums bit-exact, FP32 within the bars, the same bits through the fp32 op and a prepared activation."""
+    """Rows longer than 8192 at 5-8 columns (the matrix-core form with 8 staged activation columns, dot4 below 5
+    columns): sums bit-exact, FP32 within the bars, the same bits through the fp32 op and a prepared activation."""
     import p100_amd as P
 
     t = orc.TYPES[tname]
