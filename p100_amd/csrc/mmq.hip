@@ -126,34 +126,31 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
     // row's staged span is the dword holding the row's first byte of the step.
     auto row_shift = [&](int row, int bs) { return int((size_t(min(m0 + row, M - 1)) * nb01 + size_t(bs) * BB) & 3); };
     uint4 rw[NWL], ra[NA], rs[NS];
+    // Activation staging: piece p of the step (16 bytes) is (block p / 2BC, column p % 2BC / 2, half p % 2) and
+    // scale entry p is (block p / BC, column p % BC), so a lane's LDS write lands at p x 16 bytes: consecutive
+    // lanes, consecutive banks. (The global loads touch the same cache lines in any lane order.)
     auto load = [&](int bs) {
         const uint32_t wb = (srow_off + uint32_t(bs) * BB) & ~3u;
 #pragma unroll
         for (int k = 0; k < NWL; ++k) rw[k] = ld16(wr, wb + (sq * NWL + k) * 16);
 #pragma unroll
-        for (int j = 0; j < NA; ++j) {  // piece p: column p / 2U, 16-byte piece p % 2U of the column's 32U bytes
-            const int p = j * 64 + lane, c = p / (2 * U);
-            ra[j] = ld16(xr, c < B ? uint32_t(c * K + bs * 32 + (p % (2 * U)) * 16) : kOob);
+        for (int j = 0; j < NA; ++j) {
+            const int p = j * 64 + lane, u = p / (2 * BC), c = (p >> 1) % BC;
+            ra[j] = ld16(xr, c < B ? uint32_t(c * K + (bs + u) * 32 + (p & 1) * 16) : kOob);
         }
 #pragma unroll
-        for (int j = 0; j < NS; ++j) {  // piece p: column p / U, block p % U
-            const int p = j * 64 + lane, c = p / U;
-            rs[j] = ld16(dr, c < B ? uint32_t((c * nblk + bs + p % U) * 16) : kOob);
+        for (int j = 0; j < NS; ++j) {
+            const int p = j * 64 + lane, u = p / BC, c = p % BC;
+            rs[j] = ld16(dr, c < B ? uint32_t((c * nblk + bs + u) * 16) : kOob);
         }
     };
     auto store = [&]() {
 #pragma unroll
         for (int k = 0; k < NWL; ++k) *reinterpret_cast<uint4*>(&st.w[srow][(sq * NWL + k) * 4]) = rw[k];
 #pragma unroll
-        for (int j = 0; j < NA; ++j) {
-            const int p = j * 64 + lane, c = p / (2 * U), k16 = p % (2 * U);
-            *reinterpret_cast<uint4*>(&st.a[k16 >> 1][c][(k16 & 1) * 4]) = ra[j];
-        }
+        for (int j = 0; j < NA; ++j) reinterpret_cast<uint4*>(&st.a[0][0][0])[j * 64 + lane] = ra[j];
 #pragma unroll
-        for (int j = 0; j < NS; ++j) {
-            const int p = j * 64 + lane;
-            st.s[p % U][p / U] = __builtin_bit_cast(float4, rs[j]);
-        }
+        for (int j = 0; j < NS; ++j) (&st.s[0][0])[j * 64 + lane] = __builtin_bit_cast(float4, rs[j]);
     };
     // 16-bit field at byte offset o of staged row r.
     auto u16_at = [&](int r, int o) { return (st.w[r][o >> 2] >> (8 * (o & 2))) & 0xffffu; };
