@@ -87,9 +87,13 @@ struct MmqStage {
 
 // NW waves per work-group, each over a contiguous share of the K blocks: 8 where the grid is small (M <= 8192, at
 // most 512 work-groups, so a CU holds one and 8 waves give each SIMD two), 4 above (more work-groups per CU).
-// BC: activation columns staged (16; or 8 when at most 8 are used, which halves the activation staging so that
-// more waves fit a CU's LDS; the B operand's columns 8..15 then read columns 0..7 again and their sums are dropped).
-template <int TYPE, bool SUMS, int NW, int BC>
+// BC: activation columns staged (16; or 8 when at most 8 are used, which halves the activation staging; the B
+// operand's columns 8..15 then read columns 0..7 again and their sums are dropped). ALN: rows 16-byte aligned
+// (nb01 and the matrix base multiples of 16, as for K a multiple of 256), so with wave shares of whole steps every
+// row-step is a run of whole 16-byte chunks (144 bytes for 8 q4_0 blocks, 272 for q8_0), staged exactly: no
+// alignment shift and no overlap with the next step's span (else 4 x NWL chunks from the dword holding the
+// step's first byte).
+template <int TYPE, bool SUMS, int NW, int BC, bool ALN>
 __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict__ w, int64_t nb01, int M, int K,
                                                             int B, const int8_t* __restrict__ xq,
                                                             const float4* __restrict__ xds, float* __restrict__ y,
@@ -99,7 +103,10 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
     static_assert(U == 8 || U == 16, "activation staging covers 8 or 16 blocks per step");
     constexpr int BB = W::kBytes;
     constexpr int NWL = (U * BB + 4 + 63) / 64;  // 16-byte loads per lane (4 lanes per row)
-    constexpr int ROWDW = 16 * NWL + P1X_MMQ_PAD;  // staged dwords per row (padding spreads rows over LDS banks)
+    static_assert(!ALN || (U * BB) % 16 == 0, "aligned steps are whole 16-byte chunks");
+    constexpr int NCH = ALN ? U * BB / 16 : 4 * NWL;      // 16-byte chunks staged per row and step
+    constexpr int NLD = ALN ? (16 * NCH + 63) / 64 : NWL;  // weight loads per lane
+    constexpr int ROWDW = 4 * NCH + P1X_MMQ_PAD;  // staged dwords per row (padding spreads rows over LDS banks)
     static_assert(BC == 8 || BC == 16, "8 or 16 staged columns");
     constexpr int NA = U * BC / 32, NS = U * BC / 64;  // activation and scale loads per lane (BC columns x U blocks)
     __shared__ MmqStage<ROWDW, U, BC> stage[NW];
@@ -108,7 +115,7 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
     const int g = lane >> 4, i16 = lane & 15;
     const int m0 = blockIdx.x * 16;
     const int nblk = K / 32;
-    const int per = (nblk + NW - 1) / NW;
+    const int per = ALN ? (nblk + NW * U - 1) / (NW * U) * U : (nblk + NW - 1) / NW;
     const int b0 = min(nblk, wave * per), b1 = min(nblk, b0 + per);
     MmqStage<ROWDW, U, BC>& st = stage[wave];
 
@@ -124,15 +131,30 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
     const auto dr = rsrc(xds, uint32_t(size_t(B) * nblk * 16));
     // MFMA side: the lane's A-operand row (i16) and the rows 4g..4g+3 whose scales it applies; byte 0 of each
     // row's staged span is the dword holding the row's first byte of the step.
-    auto row_shift = [&](int row, int bs) { return int((size_t(min(m0 + row, M - 1)) * nb01 + size_t(bs) * BB) & 3); };
-    uint4 rw[NWL], ra[NA], rs[NS];
+    auto row_shift = [&](int row, int bs) {
+        return ALN ? 0 : int((size_t(min(m0 + row, M - 1)) * nb01 + size_t(bs) * BB) & 3);
+    };
+    // Aligned staging: chunk ci = k * 64 + lane of the step is chunk ci % NCH of row ci / NCH.
+    uint32_t arow_off[NLD];
+#pragma unroll
+    for (int k = 0; k < NLD; ++k) {
+        const int ci = k * 64 + lane, row = min(ci / NCH, 15);
+        arow_off[k] = uint32_t(size_t(min(m0 + row, M - 1)) * nb01) + uint32_t(ci % NCH) * 16;
+    }
+    uint4 rw[NLD], ra[NA], rs[NS];
     // Activation staging: piece p of the step (16 bytes) is (block p / 2BC, column p % 2BC / 2, half p % 2) and
     // scale entry p is (block p / BC, column p % BC), so a lane's LDS write lands at p x 16 bytes: consecutive
     // lanes, consecutive banks. (The global loads touch the same cache lines in any lane order.)
     auto load = [&](int bs) {
-        const uint32_t wb = (srow_off + uint32_t(bs) * BB) & ~3u;
+        if constexpr (ALN) {
 #pragma unroll
-        for (int k = 0; k < NWL; ++k) rw[k] = ld16(wr, wb + (sq * NWL + k) * 16);
+            for (int k = 0; k < NLD; ++k)
+                rw[k] = ld16(wr, k * 64 + lane < 16 * NCH ? arow_off[k] + uint32_t(bs) * BB : kOob);
+        } else {
+            const uint32_t wb = (srow_off + uint32_t(bs) * BB) & ~3u;
+#pragma unroll
+            for (int k = 0; k < NWL; ++k) rw[k] = ld16(wr, wb + (sq * NWL + k) * 16);
+        }
 #pragma unroll
         for (int j = 0; j < NA; ++j) {
             const int p = j * 64 + lane, u = p / (2 * BC), c = (p >> 1) % BC;
@@ -145,8 +167,16 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
         }
     };
     auto store = [&]() {
+        if constexpr (ALN) {
 #pragma unroll
-        for (int k = 0; k < NWL; ++k) *reinterpret_cast<uint4*>(&st.w[srow][(sq * NWL + k) * 4]) = rw[k];
+            for (int k = 0; k < NLD; ++k) {
+                const int ci = k * 64 + lane;
+                if (ci < 16 * NCH) *reinterpret_cast<uint4*>(&st.w[ci / NCH][(ci % NCH) * 4]) = rw[k];
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < NWL; ++k) *reinterpret_cast<uint4*>(&st.w[srow][(sq * NWL + k) * 4]) = rw[k];
+        }
 #pragma unroll
         for (int j = 0; j < NA; ++j) reinterpret_cast<uint4*>(&st.a[0][0][0])[j * 64 + lane] = ra[j];
 #pragma unroll
@@ -248,6 +278,9 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
 
 }  // namespace
 
+#ifndef P1X_MMQ_ALIGNED
+#define P1X_MMQ_ALIGNED 1  // 16-byte aligned rows stage exact chunks (ALN)
+#endif
 #ifndef P1X_MMQ_NW_NARROW
 #define P1X_MMQ_NW_NARROW 8  // waves per work-group at <= 8 columns on <= 8192 rows (8 staged columns)
 #endif
@@ -284,16 +317,24 @@ hipError_t launch_mmq(int type, int B, const void* w, int64_t nb01, int M, int K
     const dim3 grid((M + 15) / 16);
     const auto* wb = static_cast<const uint8_t*>(w);
     const auto* d4 = reinterpret_cast<const float4*>(xds);
-#define P1X_MMQ(T, S) \
+#define P1X_MMQ_L(T, S, A) \
     do {                                                                                                           \
         if (B <= 8 && M <= 8192)                                                                                   \
-            hipLaunchKernelGGL((k_mmq_mfma<T, S, P1X_MMQ_NW_NARROW, 8>), grid, dim3(64 * P1X_MMQ_NW_NARROW), 0,     \
+            hipLaunchKernelGGL((k_mmq_mfma<T, S, P1X_MMQ_NW_NARROW, 8, A>), grid, dim3(64 * P1X_MMQ_NW_NARROW), 0,  \
                                stream, wb, nb01, M, K, B, xq, d4, y, gs);                                        \
         else if (M <= 8192)                                                                                        \
-            hipLaunchKernelGGL((k_mmq_mfma<T, S, 8, 16>), grid, dim3(512), 0, stream, wb, nb01, M, K, B, xq, d4, y, gs); \
+            hipLaunchKernelGGL((k_mmq_mfma<T, S, 8, 16, A>), grid, dim3(512), 0, stream, wb, nb01, M, K, B, xq, d4, y, \
+                               gs);                                                                              \
         else                                                                                                       \
-            hipLaunchKernelGGL((k_mmq_mfma<T, S, 4, 16>), grid, dim3(256), 0, stream, wb, nb01, M, K, B, xq, d4, y, gs); \
+            hipLaunchKernelGGL((k_mmq_mfma<T, S, 4, 16, A>), grid, dim3(256), 0, stream, wb, nb01, M, K, B, xq, d4, y, \
+                               gs);                                                                              \
     } while (0)
+#define P1X_MMQ(T, S)                        \
+    do {                                     \
+        if (aligned) P1X_MMQ_L(T, S, true);  \
+        else P1X_MMQ_L(T, S, false);         \
+    } while (0)
+    const bool aligned = P1X_MMQ_ALIGNED && nb01 % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
     if (type == Q4_0) {
         if (gs) P1X_MMQ(Q4_0, true);
         else P1X_MMQ(Q4_0, false);
@@ -304,6 +345,7 @@ hipError_t launch_mmq(int type, int B, const void* w, int64_t nb01, int M, int K
         return hipErrorInvalidValue;
     }
 #undef P1X_MMQ
+#undef P1X_MMQ_L
     return hipGetLastError();
 }
 
