@@ -58,6 +58,9 @@ struct MfmaW<Q8_0> {
 #endif
 template <int TYPE>
 constexpr int step_blocks() { return TYPE == Q4_0 ? P1X_MMQ_STEP_Q4_0 : 8; }
+#ifndef P1X_MMQ_PF
+#define P1X_MMQ_PF 1  // steps whose loads are in flight per wave (1 or 2; 2 measured slower)
+#endif
 #ifndef P1X_MMQ_UNROLL
 #define P1X_MMQ_UNROLL 8  // blocks of a step unrolled together (more keeps too many operands live)
 #endif
@@ -141,46 +144,49 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
         const int ci = k * 64 + lane, row = min(ci / NCH, 15);
         arow_off[k] = uint32_t(size_t(min(m0 + row, M - 1)) * nb01) + uint32_t(ci % NCH) * 16;
     }
-    uint4 rw[NLD], ra[NA], rs[NS];
+    constexpr int PF = P1X_MMQ_PF;  // steps in flight: register sets, refilled PF steps ahead
+    uint4 rw[PF][NLD], ra[PF][NA], rs[PF][NS];
     // Activation staging: piece p of the step (16 bytes) is (block p / 2BC, column p % 2BC / 2, half p % 2) and
     // scale entry p is (block p / BC, column p % BC), so a lane's LDS write lands at p x 16 bytes: consecutive
     // lanes, consecutive banks. (The global loads touch the same cache lines in any lane order.)
-    auto load = [&](int bs) {
+    auto load = [&](int bs, auto slot_tag) {
+        constexpr int S = decltype(slot_tag)::value;
         if constexpr (ALN) {
 #pragma unroll
             for (int k = 0; k < NLD; ++k)
-                rw[k] = ld16(wr, k * 64 + lane < 16 * NCH ? arow_off[k] + uint32_t(bs) * BB : kOob);
+                rw[S][k] = ld16(wr, k * 64 + lane < 16 * NCH ? arow_off[k] + uint32_t(bs) * BB : kOob);
         } else {
             const uint32_t wb = (srow_off + uint32_t(bs) * BB) & ~3u;
 #pragma unroll
-            for (int k = 0; k < NWL; ++k) rw[k] = ld16(wr, wb + (sq * NWL + k) * 16);
+            for (int k = 0; k < NWL; ++k) rw[S][k] = ld16(wr, wb + (sq * NWL + k) * 16);
         }
 #pragma unroll
         for (int j = 0; j < NA; ++j) {
             const int p = j * 64 + lane, u = p / (2 * BC), c = (p >> 1) % BC;
-            ra[j] = ld16(xr, c < B ? uint32_t(c * K + (bs + u) * 32 + (p & 1) * 16) : kOob);
+            ra[S][j] = ld16(xr, c < B ? uint32_t(c * K + (bs + u) * 32 + (p & 1) * 16) : kOob);
         }
 #pragma unroll
         for (int j = 0; j < NS; ++j) {
             const int p = j * 64 + lane, u = p / BC, c = p % BC;
-            rs[j] = ld16(dr, c < B ? uint32_t((c * nblk + bs + u) * 16) : kOob);
+            rs[S][j] = ld16(dr, c < B ? uint32_t((c * nblk + bs + u) * 16) : kOob);
         }
     };
-    auto store = [&]() {
+    auto store = [&](auto slot_tag) {
+        constexpr int S = decltype(slot_tag)::value;
         if constexpr (ALN) {
 #pragma unroll
             for (int k = 0; k < NLD; ++k) {
                 const int ci = k * 64 + lane;
-                if (ci < 16 * NCH) *reinterpret_cast<uint4*>(&st.w[ci / NCH][(ci % NCH) * 4]) = rw[k];
+                if (ci < 16 * NCH) *reinterpret_cast<uint4*>(&st.w[ci / NCH][(ci % NCH) * 4]) = rw[S][k];
             }
         } else {
 #pragma unroll
-            for (int k = 0; k < NWL; ++k) *reinterpret_cast<uint4*>(&st.w[srow][(sq * NWL + k) * 4]) = rw[k];
+            for (int k = 0; k < NWL; ++k) *reinterpret_cast<uint4*>(&st.w[srow][(sq * NWL + k) * 4]) = rw[S][k];
         }
 #pragma unroll
-        for (int j = 0; j < NA; ++j) reinterpret_cast<uint4*>(&st.a[0][0][0])[j * 64 + lane] = ra[j];
+        for (int j = 0; j < NA; ++j) reinterpret_cast<uint4*>(&st.a[0][0][0])[j * 64 + lane] = ra[S][j];
 #pragma unroll
-        for (int j = 0; j < NS; ++j) (&st.s[0][0])[j * 64 + lane] = __builtin_bit_cast(float4, rs[j]);
+        for (int j = 0; j < NS; ++j) (&st.s[0][0])[j * 64 + lane] = __builtin_bit_cast(float4, rs[S][j]);
     };
     // 16-bit field at byte offset o of staged row r.
     auto u16_at = [&](int r, int o) { return (st.w[r][o >> 2] >> (8 * (o & 2))) & 0xffffu; };
@@ -225,36 +231,45 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
             }
         }
     };
-    if (b0 < b1) {
-        load(b0);
-        for (int bs = b0; bs < b1; bs += U) {
-            // The wave's own LDS area: the previous step's reads complete before these writes, and these writes
-            // before this step's reads (other lanes of the wave read them).
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            store();
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            // The step's weight scales, decoded once: lane (row lane % 16, blocks lane / 16 + 4 k).
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, PF - 1>;
+    // One step from register set S: stage it, decode its scales, refill S PF steps ahead, compute.
+    auto step = [&](int bs, auto slot_tag) {
+        // The wave's own LDS area: the previous step's reads complete before these writes, and these writes
+        // before this step's reads (other lanes of the wave read them).
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        store(slot_tag);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // The step's weight scales, decoded once: lane (row lane % 16, blocks lane / 16 + 4 k).
 #pragma unroll
-            for (int k = 0; k < U / 4; ++k) {
-                const int row = lane & 15, u = (lane >> 4) + 4 * k;
-                st.dw[u][row] = half_bits_to_float(u16_at(row, row_shift(row, bs) + u * BB));
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            load(bs + U);  // the next step's loads are in flight while this one computes (past b1: never used)
-            const int sh = row_shift(i16, bs);
-            if (bs + U <= b1) {
+        for (int k = 0; k < U / 4; ++k) {
+            const int row = lane & 15, u = (lane >> 4) + 4 * k;
+            st.dw[u][row] = half_bits_to_float(u16_at(row, row_shift(row, bs) + u * BB));
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        load(bs + PF * U, slot_tag);  // in flight while this step and the next compute (past b1: never used)
+        const int sh = row_shift(i16, bs);
+        if (bs + U <= b1) {
 #pragma unroll P1X_MMQ_UNROLL
-                for (int u = 0; u < U; ++u) block(bs, u, sh, std::false_type{});
-            } else {
+            for (int u = 0; u < U; ++u) block(bs, u, sh, std::false_type{});
+        } else {
 #pragma unroll P1X_MMQ_UNROLL
-                for (int u = 0; u < U; ++u) block(bs, u, sh, std::true_type{});
-            }
+            for (int u = 0; u < U; ++u) block(bs, u, sh, std::true_type{});
+        }
+    };
+    if (b0 < b1) {
+        load(b0, I0{});
+        if constexpr (PF == 2) load(b0 + U, I1{});
+        for (int bs = b0; bs < b1; bs += PF * U) {
+            step(bs, I0{});
+            if constexpr (PF == 2)
+                if (bs + U < b1) step(bs + U, I1{});
         }
     }
 
