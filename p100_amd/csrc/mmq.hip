@@ -109,7 +109,9 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
     static_assert(!ALN || (U * BB) % 16 == 0, "aligned steps are whole 16-byte chunks");
     constexpr int NCH = ALN ? U * BB / 16 : 4 * NWL;      // 16-byte chunks staged per row and step
     constexpr int NLD = ALN ? (16 * NCH + 63) / 64 : NWL;  // weight loads per lane
-    constexpr int ROWDW = 4 * NCH + P1X_MMQ_PAD;  // staged dwords per row (padding spreads rows over LDS banks)
+    // Staged dwords per row. Padding spreads the 16 rows over LDS banks: aligned rows take a stride of 4 x an odd
+    // count (16 distinct banks for the A-operand reads of one dword offset, whole 16-byte chunks kept aligned).
+    constexpr int ROWDW = ALN ? 4 * (NCH | 1) : 4 * NCH + P1X_MMQ_PAD;
     static_assert(BC == 8 || BC == 16, "8 or 16 staged columns");
     constexpr int NA = U * BC / 32, NS = U * BC / 64;  // activation and scale loads per lane (BC columns x U blocks)
     __shared__ MmqStage<ROWDW, U, BC> stage[NW];
