@@ -249,20 +249,26 @@ struct UnitQ6_K {
     }
     __device__ __forceinline__ float acc(const ActBlock* x, float a, int32_t* g) const {
         const int nsh = (s & 2) ? 4 : 0, hsh = 2 * (s & 3);
-        uint32_t q6[8];
+        // The 6-bit codes v (0..63) are non-negative int8 as they are, so the signed dot4 takes them unchanged and
+        // the -32 of every code becomes -32 * sum(x) per 16-element half: sum(x_lo) by dot4 with ones, sum(x_hi)
+        // from the block's exact isum. The int32 sums are the same integers as those of (v - 32) . x.
+        uint32_t v6[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t v = ((ql[j] >> nsh) & kLo) | (((qh[j] >> hsh) & 0x03030303u) << 4);  // 0..63 per byte
-            q6[j] = ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u;                             // v - 32 per byte
-        }
-        int g0 = dot4(int(q6[0]), x[0].lo.x, 0);
-        g0 = dot4(int(q6[1]), x[0].lo.y, g0);
-        g0 = dot4(int(q6[2]), x[0].lo.z, g0);
-        g0 = dot4(int(q6[3]), x[0].lo.w, g0);
-        int g1 = dot4(int(q6[4]), x[0].hi.x, 0);
-        g1 = dot4(int(q6[5]), x[0].hi.y, g1);
-        g1 = dot4(int(q6[6]), x[0].hi.z, g1);
-        g1 = dot4(int(q6[7]), x[0].hi.w, g1);
+        for (int j = 0; j < 8; ++j) v6[j] = ((ql[j] >> nsh) & kLo) | (((qh[j] >> hsh) & 0x03030303u) << 4);
+        constexpr int kOnes = 0x01010101;
+        int slo = dot4(kOnes, x[0].lo.x, 0);
+        slo = dot4(kOnes, x[0].lo.y, slo);
+        slo = dot4(kOnes, x[0].lo.z, slo);
+        slo = dot4(kOnes, x[0].lo.w, slo);
+        const int shi = int(x[0].ds.z) - slo;  // isum is exact in the float
+        int g0 = dot4(int(v6[0]), x[0].lo.x, -32 * slo);
+        g0 = dot4(int(v6[1]), x[0].lo.y, g0);
+        g0 = dot4(int(v6[2]), x[0].lo.z, g0);
+        g0 = dot4(int(v6[3]), x[0].lo.w, g0);
+        int g1 = dot4(int(v6[4]), x[0].hi.x, -32 * shi);
+        g1 = dot4(int(v6[5]), x[0].hi.y, g1);
+        g1 = dot4(int(v6[6]), x[0].hi.z, g1);
+        g1 = dot4(int(v6[7]), x[0].hi.w, g1);
         g[0] = g0;
         g[1] = g1;
         const int sc0 = int(int8_t(sw & 255)), sc1 = int(int8_t((sw >> 8) & 255));
