@@ -161,13 +161,16 @@ struct KvQuant {
         doff = boff - (boff & ~3u);
         nib_shift = (KT == kKvQ4_0 && jq >= 2) ? 4u : 0u;
     }
-    // The lane's 8 values (as exact small integers) and the block scale.
-    __device__ __forceinline__ void to_f32(uint4 w, float* out, float& d) const {
+    // The lane's 8 codes, one conversion each, and the block scale: value = d * (out + kOff). q4_0 nibbles go in
+    // as unsigned bytes (q + 8, offset -8 applied once per key for K and once at the end for V); q8_0 codes as
+    // signed bytes (offset 0: flipping the sign bit to convert unsigned bytes measured slower).
+    static constexpr float kOff = KT == kKvQ8_0 ? 0.0f : -8.0f;
+    __device__ __forceinline__ void to_ubyte_f32(uint4 w, float* out, float& d) const {
         const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
         const int i0 = int(qoff >> 2);
         const uint32_t sel = (qoff & 2) ? 0x05040302u : 0x03020100u;
-        const uint32_t lo = __builtin_amdgcn_perm(i0 ? ww[2] : ww[1], i0 ? ww[1] : ww[0], sel);
-        const uint32_t hi = __builtin_amdgcn_perm(i0 ? ww[3] : ww[2], i0 ? ww[2] : ww[1], sel);
+        uint32_t lo = __builtin_amdgcn_perm(i0 ? ww[2] : ww[1], i0 ? ww[1] : ww[0], sel);
+        uint32_t hi = __builtin_amdgcn_perm(i0 ? ww[3] : ww[2], i0 ? ww[2] : ww[1], sel);
         if constexpr (KT == kKvQ8_0) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -175,11 +178,12 @@ struct KvQuant {
                 out[4 + k] = float(int8_t((hi >> (8 * k)) & 0xffu));
             }
         } else {
-            const uint32_t l4 = (lo >> nib_shift) & 0x0F0F0F0Fu, h4 = (hi >> nib_shift) & 0x0F0F0F0Fu;
+            lo = (lo >> nib_shift) & 0x0F0F0F0Fu;
+            hi = (hi >> nib_shift) & 0x0F0F0F0Fu;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                out[k] = float((l4 >> (8 * k)) & 0xffu) - 8.0f;
-                out[4 + k] = float((h4 >> (8 * k)) & 0xffu) - 8.0f;
+                out[k] = float((lo >> (8 * k)) & 0xffu);
+                out[4 + k] = float((hi >> (8 * k)) & 0xffu);
             }
         }
         const int d16 = int((w.x >> (8 * doff)) & 0xffffu);  // meaningful in the block's first lane
@@ -244,14 +248,21 @@ __global__ __launch_bounds__(kSplitThreads) void k_fa_split(FaArgs a) {
             r[4] = x1.x * qmul; r[5] = x1.y * qmul; r[6] = x1.z * qmul; r[7] = x1.w * qmul;
         }
     }
-    // Softmax state: a wave-uniform reference max per head, and per-lane partial sums (group-local keys).
-    float mref[NH], s[NH], o[NH][DPL];
+    // Softmax state: a wave-uniform reference max per head, and per-lane partial sums (group-local keys). For a
+    // quantized cache also the lane's sum of q per head (the K codes' offset term) and the running sum of p * d
+    // over its V blocks (the V codes' offset term, added to O once at the end).
+    float mref[NH], s[NH], o[NH][DPL], qsum[NH], pdsum[NH];
 #pragma unroll
     for (int hh = 0; hh < NH; ++hh) {
         mref[hh] = -INFINITY;
         s[hh] = 0.0f;
+        pdsum[hh] = 0.0f;
+        qsum[hh] = 0.0f;
 #pragma unroll
-        for (int d = 0; d < DPL; ++d) o[hh][d] = 0.0f;
+        for (int d = 0; d < DPL; ++d) {
+            o[hh][d] = 0.0f;
+            if constexpr (KT != kKvF16) qsum[hh] += qr[hh][d];
+        }
     }
     // f16: element strides; quantized: byte strides from the byte pointers kq / vq.
     const auto krs = KT == kKvF16 ? kv_rsrc(a.k + size_t(b) * a.k_batch + size_t(kvh) * a.k_head, a.k_bytes)
@@ -262,7 +273,8 @@ __global__ __launch_bounds__(kSplitThreads) void k_fa_split(FaArgs a) {
                                   : kv_rsrc(reinterpret_cast<const __half*>(a.vq + size_t(b) * a.v_batch +
                                                                             size_t(kvh) * a.v_head),
                                             a.v_bytes);
-    const KvQuant<KT == kKvF16 ? kKvQ8_0 : KT> kvq(l);
+    using KvQ = KvQuant<KT == kKvF16 ? kKvQ8_0 : KT>;
+    const KvQ kvq(l);
     const float* mrow = kMask ? a.mask + size_t(i) * a.seq_kv : nullptr;
 
     // Key of (batch t, slot u) for this lane's group: the GPW groups of a wave read GPW consecutive rows.
@@ -301,7 +313,7 @@ __global__ __launch_bounds__(kSplitThreads) void k_fa_split(FaArgs a) {
 #pragma unroll
                 for (int c = 0; c < CH; ++c) h8_to_f32(bf.k[u][c], kf + 8 * c);
             } else {
-                kvq.to_f32(bf.k[u][0], kf, dk);
+                kvq.to_ubyte_f32(bf.k[u][0], kf, dk);
             }
 #pragma unroll
             for (int hh = 0; hh < NH; ++hh) {
@@ -311,7 +323,10 @@ __global__ __launch_bounds__(kSplitThreads) void k_fa_split(FaArgs a) {
                     d0 = fmaf(qr[hh][d], kf[d], d0);
                     d1 = fmaf(qr[hh][DPL / 2 + d], kf[DPL / 2 + d], d1);
                 }
-                x[u][hh] = key_sum<LPK>(KT == kKvF16 ? d0 + d1 : (d0 + d1) * dk);
+                // Quantized: the codes' offset times the lane's sum of q, then the block scale (per lane quad).
+                float part = d0 + d1;
+                if constexpr (KT != kKvF16 && KvQ::kOff != 0.0f) part = fmaf(KvQ::kOff, qsum[hh], part);
+                x[u][hh] = key_sum<LPK>(KT == kKvF16 ? part : part * dk);
             }
             const int j = key0 + t * KPB + u * GPW;
             const bool ok = !kLast || j < j1;
@@ -342,6 +357,7 @@ __global__ __launch_bounds__(kSplitThreads) void k_fa_split(FaArgs a) {
                 const float mn = fmaxf(mref[hh], wave_group_max<LPK>(bm));  // the same value in every lane
                 const float alpha = mref[hh] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mref[hh] - mn);
                 s[hh] *= alpha;
+                pdsum[hh] *= alpha;
 #pragma unroll
                 for (int d = 0; d < DPL; ++d) o[hh][d] *= alpha;
                 mref[hh] = mn;
@@ -355,13 +371,15 @@ __global__ __launch_bounds__(kSplitThreads) void k_fa_split(FaArgs a) {
 #pragma unroll
                 for (int c = 0; c < CH; ++c) h8_to_f32(bf.v[u][c], vf[u] + 8 * c);
             } else {
-                kvq.to_f32(bf.v[u][0], vf[u], dv[u]);
+                kvq.to_ubyte_f32(bf.v[u][0], vf[u], dv[u]);
             }
             if constexpr (kLast) {  // rows past the visible end may hold NaN / Inf bits: select zeros (p is 0)
                 const bool ok = key0 + t * KPB + u * GPW < j1;
                 dv[u] = ok ? dv[u] : 0.0f;
+                if constexpr (KT == kKvF16) {  // (byte codes are always finite)
 #pragma unroll
-                for (int d = 0; d < DPL; ++d) vf[u][d] = ok ? vf[u][d] : 0.0f;
+                    for (int d = 0; d < DPL; ++d) vf[u][d] = ok ? vf[u][d] : 0.0f;
+                }
             }
         }
 #pragma unroll
@@ -373,7 +391,10 @@ __global__ __launch_bounds__(kSplitThreads) void k_fa_split(FaArgs a) {
             for (int u = 0; u < kKeys; ++u) {
                 p[u] = __builtin_amdgcn_exp2f(x[u][hh] - base);
                 s[hh] += p[u];
-                if constexpr (KT != kKvF16) p[u] *= dv[u];  // d of the lane's V block folded into p
+                if constexpr (KT != kKvF16) {  // d of the lane's V block folded into p; the codes' offset later
+                    p[u] *= dv[u];
+                    if constexpr (KvQ::kOff != 0.0f) pdsum[hh] += p[u];
+                }
             }
 #pragma unroll
             for (int d = 0; d < DPL; ++d) {
@@ -407,6 +428,12 @@ __global__ __launch_bounds__(kSplitThreads) void k_fa_split(FaArgs a) {
     for (int p = 0; p < PF - 1; ++p)
         if (t0 + p < nb) step(ring[p], t0 + p);
 
+    if constexpr (KT != kKvF16 && KvQ::kOff != 0.0f) {  // the V codes' offset: value = d * (code + kOff)
+#pragma unroll
+        for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) o[hh][d] = fmaf(KvQ::kOff, pdsum[hh], o[hh][d]);
+    }
     // The groups of a wave share its reference max, so their partial sums merge by plain addition: the groups
     // of one 16-lane row with DPP rotations, then through LDS, one state per 16-lane row (or per group when a
     // group spans two rows), across the 4 waves.
