@@ -160,13 +160,14 @@ def test_mmvq_parity(orc, gpu, tname):
 @pytest.mark.parametrize("tname", ["q4_0", "q8_0"])
 def test_many_columns_parity(orc, gpu, tname):
     """9..16 activation columns (the int8 matrix-core form): int32 group sums bit-exact, FP32 within the bars;
-    K of one and two blocks (idle waves in the K split), partial 16-row tiles, a full-size shape, and q8_0 matrices
-    whose byte size ends mid-dword (odd block counts: the last row's last block is read through the rounded range)."""
+    K of one and two blocks (idle waves in the K split), partial 16-row tiles, a full-size shape, q8_0 matrices
+    whose byte size ends mid-dword (odd block counts: the last row's last block is read through the rounded range),
+    and 16-byte aligned rows (K a multiple of 256: exact-chunk staging) both up to and past 8192 rows."""
     import p100_amd as P
 
     t = orc.TYPES[tname]
     for k, rows in ((32, 17), (64, 33), (96, 16), (96, 17), (4128, 17), (4096, 17), (14336, 33), (4096, 4096),
-                    (64, 8232)):
+                    (64, 8232), (256, 8200)):
         for ncols in ((9, 12, 16) if rows < 4096 else (16,)):  # up to 8192 rows 8 waves per work-group, then 4
             w, x = make_case(orc, t, k, rows, ncols, seed=900 + k + rows + ncols)
             y, sums = P.mul_mat_vec(t, to_dev(w), rows, k, to_dev(x), act="q8_1", group_sums=True)
