@@ -22,6 +22,7 @@ import argparse
 import ctypes as C
 import json
 import os
+import pathlib
 import sys
 import time
 
@@ -112,6 +113,9 @@ def main():
                                                    "q4_K:4096x14336)")
     ap.add_argument("--cols", type=int, nargs="+", default=[4, 16])
     ap.add_argument("--fa-ctx", type=int, nargs="+", default=[512, 640, 2048, 8192, 32768])
+    ap.add_argument("--tbo-sql", default=None, metavar="PATH",
+                    help="also write the mat-vec sweep and the FA legs as test-backend-ops perf rows (the SQL that "
+                         "the reference's bin/mm-gbps.py and bench/analyze.py read)")
     ap.add_argument("--fa-kernel", choices=("auto", "split", "mc"), default="auto",
                     help="first-pass attention kernel (p1x_fa_select_kernel): the automatic choice, the vector "
                          "pass, or the matrix-core alternative")
@@ -197,6 +201,8 @@ def main():
                                                      kvlen_runs=not args.fa_fp16_only)}
         for kv_type in () if args.fa_fp16_only else ("q8_0", "q4_0"):
             rec[f"fa_decode_{kv_type}_kv"] = measure_fa_quant(torch, P, lib, synth, timer, gen, args.fa_ctx, kv_type)
+        if args.tbo_sql:
+            write_tbo_sql(args.tbo_sql, rec, torch.cuda.get_device_name(0))
         print(json.dumps(rec))
         return
 
@@ -269,7 +275,58 @@ def main():
         result["extra"] = extra_measurements(torch, P, lib, synth, timer, gen, layers, xs, args.fa_ctx)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(P, layers[0]["down"], xs[14336], args.cpu_seconds)
+    if args.tbo_sql:
+        write_tbo_sql(args.tbo_sql, result.get("extra", {}), torch.cuda.get_device_name(0))
     print(json.dumps(result), flush=True)
+
+
+# test-backend-ops perf rows (the schema of the reference's tests/fixtures/tbo-perf-cpu.sql:1-18), so that the
+# reference's own analysis scripts read this bench: MUL_MAT cases keyed by type_a, m, n, k with an unbatched,
+# contiguous f32 right-hand side (bin/mm-gbps.py:24-31), FLASH_ATTN_EXT cases in test-backend-ops' parameter
+# spelling. time_us is the measured graph period of the op; memory_kb the algorithmic bytes.
+TBO_COLUMNS = ("test_time", "build_commit", "backend_name", "op_name", "op_params", "test_mode", "supported",
+               "passed", "error_message", "time_us", "flops", "bandwidth_gb_s", "memory_kb", "n_runs",
+               "device_description", "backend_reg_name")
+
+
+def tbo_rows(extra):
+    """(op_name, op_params, time_us, bytes, flops) for each mat-vec sweep point and FA context in `extra`."""
+    rows = []
+    for key, rec in extra.get("matvec_sweep_op_us", {}).items():  # "q4_0 4096x14336 n=1"
+        tname, shape, ncols = key.split()
+        m, k = (int(v) for v in shape.split("x"))
+        n = int(ncols.split("=")[1])
+        blk, per = {"q4_0": (18, 32), "q8_0": (34, 32), "q4_K": (144, 256), "q6_K": (210, 256)}[tname]
+        nbytes = m * k // per * blk + n * k * 4 + m * n * 4  # bin/mm-gbps.py:51-57
+        params = (f"type_a={tname},type_b=f32,m={m},n={n},k={k},bs=[1,1],nr=[1,1],per=[0,1,2,3],k_v=0,o=1,"
+                  "src_overlap=0,m_v=0,pad=0")
+        rows.append(("MUL_MAT", params, rec["us"], nbytes, 2.0 * m * n * k))
+    for name, kv_type in (("fa_decode", "f16"), ("fa_decode_q8_0_kv", "q8_0"), ("fa_decode_q4_0_kv", "q4_0")):
+        for ctx, rec in extra.get(name, {}).get("by_ctx", {}).items():
+            kv = int(ctx)
+            params = (f"hsk=128,hsv=128,nh=8,nr23=[4,1],kv={kv},nb=1,mask=0,sinks=0,max_bias=0.000000,"
+                      f"logit_softcap=0.000000,prec=f32,type_K={kv_type},type_V={kv_type},permute=[0,1,2,3],"
+                      "kv_view=0,v_is_view_of_k=0,n_kv_max=0")
+            rows.append(("FLASH_ATTN_EXT", params, rec["us"], rec.get("bytes", 0), 4.0 * 32 * 128 * kv))
+    return rows
+
+
+def write_tbo_sql(path, extra, device):
+    import datetime
+
+    now = datetime.datetime.now(datetime.timezone.utc).strftime("%Y-%m-%dT%H:%M:%SZ")
+    kinds = {"supported": "INTEGER", "passed": "INTEGER", "memory_kb": "INTEGER", "n_runs": "INTEGER",
+             "time_us": "REAL", "flops": "REAL", "bandwidth_gb_s": "REAL"}
+    lines = ["CREATE TABLE IF NOT EXISTS test_backend_ops (",
+             ",\n".join(f"  {c} {kinds.get(c, 'TEXT')}" for c in TBO_COLUMNS), ");", ""]
+    for op, params, us, nbytes, flops in tbo_rows(extra):
+        vals = (now, "p100_amd", "ROCm0", op, params, "perf", "1", "1", "", f"{us:.6f}",
+                f"{flops / (us * 1e-6):.6f}", f"{nbytes / (us * 1e-6) / 1e9:.6f}", str(nbytes // 1024), "1",
+                device, "ROCm")
+        lines.append(f"INSERT INTO test_backend_ops ({', '.join(TBO_COLUMNS)}) VALUES "
+                     f"({', '.join(repr(v) for v in vals)});")
+    pathlib.Path(path).write_text("\n".join(lines) + "\n")
+    log(f"[bench] wrote {len(lines) - 4} test-backend-ops rows to {path}")
 
 
 def measure_roofline(torch, P, lib, timer, gen, x):
