@@ -308,6 +308,12 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
 #ifndef P1X_MMQ_MIN_COLS_LONG_Q8_0
 #define P1X_MMQ_MIN_COLS_LONG_Q8_0 5  // (q8_0)
 #endif
+#ifndef P1X_MMQ_WIDE_NARROW
+#define P1X_MMQ_WIDE_NARROW 1  // more than 8192 rows at <= 8 columns: 4 waves staging 8 columns
+#endif
+#ifndef P1X_MMQ_MIN_COLS_SHORT
+#define P1X_MMQ_MIN_COLS_SHORT 7  // columns from which rows of at most 8192 on >= 4096 rows take the matrix cores
+#endif
 #ifndef P1X_MMQ_MIN_COLS
 #define P1X_MMQ_MIN_COLS 9  // columns from which the matrix-core form replaces the dot4 kernels
 #endif
@@ -318,15 +324,20 @@ bool mmq_fits(int M, int64_t nb01, int K, int B) {
     return int64_t(M) * nb01 + 3 <= int64_t(kOob) && int64_t(B) * K <= int64_t(kOob) &&
            int64_t(B) * (K / 32) * 16 <= int64_t(kOob);
 }
-// From 9 columns always; also rows longer than 8192 on at most 8192 rows (the 8-wave form) from 5 columns, where
-// the dot4 kernel's LDS-staged activation (B x 14336 x 1.5 bytes per work-group) outweighs it (4096x14336, graph
-// period, dot4 against the 8-column-staging matrix-core form at 4 / 5 / 6 / 7 / 8 columns: q4_0 15.0 / 24.3 / 27.0
-// (dot4) against 17.4 / 16.9 / 17.0 / 17.2 / 17.2 us; q8_0 18.9 (dot4, 4 columns) against 20.7 / 21.0 / 21.3 /
-// 21.5 / 21.7 us). K <= 8192 stays on dot4 up to 8 columns (e.g. 4096x4096 at 8 columns 8.5 against 9.5 us).
+// From 9 columns always. Below that, measured per shape (graph period of the kernel on a prepared activation,
+// dot4 against the matrix-core form): rows longer than 8192 on at most 8192 rows from 5 columns, where the dot4
+// kernel's LDS-staged activation (B x 14336 x 1.5 bytes per work-group) outweighs it (4096x14336: q4_0 at 4 / 5
+// / 6 / 8 columns 15.0 / 24.3 / 27.0 / - against 17.4 / 16.9 / 17.0 / 17.2 us; q8_0 at 4 columns 18.9 against
+// 20.7, then 21.0-21.7 for the matrix cores); rows of at most 8192 on at least 4096 rows from 7 columns (5 / 6 /
+// 8 columns, dot4 against matrix cores: q4_0 14336x4096 13.0 / 15.2 / 18.2 against 16.8 / 17.0 / 17.2, 4096x4096
+// 6.2 / 6.7 / 7.5 against 6.6 / 6.7 / 6.8; q8_0 14336x4096 18.2 / 19.8 / 24.7 against 19.7 / 19.9 / 20.3,
+// 4096x4096 7.4 / 7.7 / 9.3 against 7.6 / 7.7 / 8.0 us); fewer rows stay on dot4 (1024x4096 at 8 columns 3.8 against
+// 5.9 us).
 bool mmq_preferred(int type, int B, int M, int K) {
     if (!mmq_supported(type, B)) return false;
     if (B >= P1X_MMQ_MIN_COLS) return true;
-    return K > 8192 && M <= 8192 && B >= (type == Q8_0 ? P1X_MMQ_MIN_COLS_LONG_Q8_0 : P1X_MMQ_MIN_COLS_LONG_Q4_0);
+    if (K > 8192) return M <= 8192 && B >= (type == Q8_0 ? P1X_MMQ_MIN_COLS_LONG_Q8_0 : P1X_MMQ_MIN_COLS_LONG_Q4_0);
+    return M >= 4096 && B >= P1X_MMQ_MIN_COLS_SHORT;
 }
 
 hipError_t launch_mmq(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
@@ -341,6 +352,9 @@ hipError_t launch_mmq(int type, int B, const void* w, int64_t nb01, int M, int K
                                stream, wb, nb01, M, K, B, xq, d4, y, gs);                                        \
         else if (M <= 8192)                                                                                        \
             hipLaunchKernelGGL((k_mmq_mfma<T, S, 8, 16, A>), grid, dim3(512), 0, stream, wb, nb01, M, K, B, xq, d4, y, \
+                               gs);                                                                              \
+        else if (B <= 8 && P1X_MMQ_WIDE_NARROW)                                                                    \
+            hipLaunchKernelGGL((k_mmq_mfma<T, S, 4, 8, A>), grid, dim3(256), 0, stream, wb, nb01, M, K, B, xq, d4, y, \
                                gs);                                                                              \
         else                                                                                                       \
             hipLaunchKernelGGL((k_mmq_mfma<T, S, 4, 16, A>), grid, dim3(256), 0, stream, wb, nb01, M, K, B, xq, d4, y, \

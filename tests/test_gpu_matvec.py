@@ -196,6 +196,25 @@ def test_long_rows_five_to_eight_columns(orc, gpu, tname):
             assert (y3.view(np.uint32) == y2.view(np.uint32)).all()
 
 
+@pytest.mark.parametrize("tname", ["q4_0", "q8_0"])
+def test_many_rows_seven_eight_columns(orc, gpu, tname):
+    """At least 4096 rows of at most 8192 elements at 7-8 columns (the matrix-core form: 8 waves per work-group up
+    to 8192 rows, 4 beyond, 8 staged activation columns), rows 16-byte aligned (K 256) and not (K 4128), with a
+    partial last row tile: sums bit-exact, FP32 within the bars, the fp32 op equal to the prepared activation's."""
+    import p100_amd as P
+
+    t = orc.TYPES[tname]
+    for k, rows in ((256, 4104), (256, 8200), (4128, 8200)):
+        for ncols in (7, 8):
+            w, x = make_case(orc, t, k, rows, ncols, seed=1900 + k + rows + ncols)
+            y, sums = P.mul_mat_vec(t, to_dev(w), rows, k, to_dev(x), act="q8_1", group_sums=True)
+            check_matvec(orc, t, w, x, y.cpu().numpy(), sums.cpu().numpy(), "q81")
+            y2 = P.mul_mat_vec(t, to_dev(w), rows, k, to_dev(x), act="q8_1").cpu().numpy()
+            y3 = P.mul_mat_vec(t, to_dev(w), rows, k, P.quantize_q8_1(to_dev(x))).cpu().numpy()
+            assert (y2.view(np.uint32) == y.cpu().numpy().view(np.uint32)).all()
+            assert (y3.view(np.uint32) == y2.view(np.uint32)).all()
+
+
 @pytest.mark.parametrize("tname", TYPES)
 @pytest.mark.parametrize("scale", [1e5, 1e-5])
 def test_mmvq_activation_ranges(orc, gpu, tname, scale):
