@@ -90,7 +90,7 @@ int check_matvec(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K, i
     if (M <= 0 || K <= 0 || M > INT32_MAX || K > INT32_MAX) return fail(P1X_EINVAL, "M and K must be in 1..INT_MAX");
     if (K % block_elems(wtype)) return fail(P1X_EINVAL, "K must be a multiple of the block size");
     if (ncols < 1 || ncols > max_cols)
-        return fail(P1X_EINVAL, max_cols == 8 ? "ncols (ne11) must be 1..8 (up to 16 for q4_0 / q8_0 with a Q8_1 activation)"
+        return fail(P1X_EINVAL, max_cols == 8 ? "ncols (ne11) must be 1..8 (up to 16 for q4_0 / q8_0 / q4_K with a Q8_1 activation)"
                                               : "ncols (ne11) must be 1..16");
     if (nb01 < K / block_elems(wtype) * block_bytes(wtype)) return fail(P1X_EINVAL, "row stride nb01 shorter than a row");
     if (nb01 % 2) return fail(P1X_EINVAL, "row stride nb01 must be even (GGUF blocks are 2-byte aligned)");
@@ -225,9 +225,11 @@ int p1x_should_use_mmvh(int wtype, int64_t M, int64_t K, int64_t ncols) {
     static const bool disable = std::getenv("P1X_DISABLE_MMVH") != nullptr;
     if (block_bytes(wtype) == 0 || M <= 0 || K <= 0 || ncols < 1 || ncols > 8) return 0;
     // Where the h16 path is the faster one on gfx950 (bench.py mmvh_vs_mmvq at the Llama-3-8B shapes): q4_K rows
-    // longer than 8192 elements at 4..8 columns (4096x14336: 36.3 / 64.8 us against 44.3 / 85.2 us for Q8_1). At
-    // every other measured shape and type the Q8_1 integer path is faster (by 1.2x to 3.8x).
-    const bool preferred = wtype == P1X_Q4_K && K > 8192 && ncols >= 4;
+    // longer than 8192 elements at 4..8 columns against the dot4 kernels (4096x14336: 42.2 / 79.2 us against
+    // 43.5 / 85.8 us), unless the int8 matrix-core form takes the shape (13.6 / 14.1 us there; from 2 columns on
+    // 4096 rows or more). At every other measured shape and type the Q8_1 integer path is faster (1.2x to 5.6x).
+    const bool mmq = M <= INT32_MAX && K <= INT32_MAX && p1x::mmq_preferred(wtype, int(ncols), int(M), int(K));
+    const bool preferred = wtype == P1X_Q4_K && K > 8192 && ncols >= 4 && !mmq;
     return force || (preferred && !disable) ? 1 : 0;
 }
 
@@ -256,9 +258,9 @@ int p1x_mul_mat_vec_q8_1(int wtype, const void* w, int64_t nb01, int64_t M, int6
     if (!qs || !ds) return fail(P1X_EINVAL, "null activation pointer");
     if (!aligned(qs, 16) || !aligned(ds, 16)) return fail(P1X_EINVAL, "qs and ds must be 16-byte aligned");
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (ncols > 8 && !p1x::mmq_fits(int(M), nb01, int(K), int(ncols)))
-        return fail(P1X_EUNSUPPORTED, "9..16 columns need the weights (M * nb01) within 2 GiB");
-    hipError_t e = p1x::mmq_preferred(wtype, int(ncols), int(M), int(K)) && p1x::mmq_fits(int(M), nb01, int(K), int(ncols))
+    if (ncols > 8 && !p1x::mmq_fits(wtype, int(M), nb01, int(K), int(ncols)))
+        return fail(P1X_EUNSUPPORTED, "9..16 columns need the weights (M * nb01) within 2 GiB and q4_K rows of 16-byte multiples");
+    hipError_t e = p1x::mmq_preferred(wtype, int(ncols), int(M), int(K)) && p1x::mmq_fits(wtype, int(M), nb01, int(K), int(ncols))
                        ? p1x::launch_mmq(wtype, int(ncols), w, nb01, int(M), int(K), qs, ds, y, group_sums, s)
                        : p1x::launch_mmvq(wtype, int(ncols), w, nb01, int(M), int(K), qs, ds, nullptr, y, group_sums, s);
     return e == hipSuccess ? P1X_OK : hip_fail(e, "mul_mat_vec_q8_1");
@@ -303,11 +305,11 @@ int p1x_mul_mat_vec(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K
     if (act_mode == P1X_ACT_Q8_1) {
         auto* qs = reinterpret_cast<int8_t*>(base);
         auto* ds = reinterpret_cast<float*>(base + align256(size_t(K) * ncols));
-        if (ncols > 8 && !p1x::mmq_fits(int(M), nb01, int(K), int(ncols)))
-            return fail(P1X_EUNSUPPORTED, "9..16 columns need the weights (M * nb01) within 2 GiB");
+        if (ncols > 8 && !p1x::mmq_fits(wtype, int(M), nb01, int(K), int(ncols)))
+            return fail(P1X_EUNSUPPORTED, "9..16 columns need the weights (M * nb01) within 2 GiB and q4_K rows of 16-byte multiples");
         hipError_t e = p1x::launch_quantize_q8_1(x, qs, ds, int(K), int(ncols), s);
         if (e != hipSuccess) return hip_fail(e, "quantize_q8_1");
-        e = p1x::mmq_preferred(wtype, int(ncols), int(M), int(K)) && p1x::mmq_fits(int(M), nb01, int(K), int(ncols))
+        e = p1x::mmq_preferred(wtype, int(ncols), int(M), int(K)) && p1x::mmq_fits(wtype, int(M), nb01, int(K), int(ncols))
                 ? p1x::launch_mmq(wtype, int(ncols), w, nb01, int(M), int(K), qs, ds, y, group_sums, s)
                 : p1x::launch_mmvq(wtype, int(ncols), w, nb01, int(M), int(K), qs, ds, nullptr, y, group_sums, s);
         return e == hipSuccess ? P1X_OK : hip_fail(e, "mul_mat_vec_q8_1");

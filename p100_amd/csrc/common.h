@@ -115,6 +115,20 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
 }
 __device__ __forceinline__ float round_fp16(float x) { return __half2float(__float2half(x)); }
 
+// q4_K six-bit scale / min codes of sub-block j (0..7) from the super-block's three scale dwords (bytes 4..15),
+// as get_scale_min_k4 (src/reference/qmv_model.cpp:72-77).
+__device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j, int& sc, int& mn) {
+    const int sh = 8 * (j & 3);
+    const uint32_t b0 = (s0 >> sh) & 255, b1 = (s1 >> sh) & 255, b2 = (s2 >> sh) & 255;
+    if (j < 4) {
+        sc = int(b0 & 63);
+        mn = int(b1 & 63);
+    } else {
+        sc = int((b2 & 15) | ((b0 >> 6) << 4));
+        mn = int((b2 >> 4) | ((b1 >> 6) << 4));
+    }
+}
+
 // Reductions over the 32 lanes of a wave half (one 32-element activation block): the xor butterfly with offsets
 // 16, 8, 4, 2, 1, the exact FP32 order of the reference (src/reference/qmv_model.cpp:44-52). Since a+b == b+a in
 // IEEE arithmetic, every lane of the half ends with the same, order-defined result.

@@ -70,12 +70,12 @@ hipError_t launch_mmvq_swiglu(int type, const void* w, int64_t nb01, int F, int 
 bool mmvq_rope_kv_supported(int type, int M, int K, int d);
 hipError_t launch_mmvq_rope_kv(int type, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
                                const RopeKv& rk, hipStream_t stream);
-// Several activation columns on int8 matrix cores (mmq.hip): q4_0 / q8_0 weights, 1..kMmqMaxCols columns of a
+// Several activation columns on int8 matrix cores (mmq.hip): q4_0 / q8_0 / q4_K weights, 1..kMmqMaxCols columns of a
 // prepared Q8_1 activation.
 constexpr int kMmqMaxCols = 16;
 bool mmq_supported(int type, int B);
 bool mmq_preferred(int type, int B, int M, int K);  // the form chosen for B columns (always for B > 8)
-bool mmq_fits(int M, int64_t nb01, int K, int B);  // weight and activation byte ranges within 32-bit buffer offsets
+bool mmq_fits(int type, int M, int64_t nb01, int K, int B);  // byte ranges within 32-bit buffer offsets; row layout
 hipError_t launch_mmq(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
                       float* y, int32_t* gs, hipStream_t stream);
 hipError_t launch_mmvh(int type, int B, const void* w, int64_t nb01, int M, int K, const uint16_t* h,

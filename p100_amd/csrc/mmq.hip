@@ -4,7 +4,8 @@
 // v_mfma_i32_16x16x32_i8, so one instruction yields the exact int32 block sums of 16 weight rows x 16 columns
 // (the reference's per-block integer dot products, bit for bit); each block's sums are then scaled in FP32 with
 // the same per-block formula as the dot4 path (src/reference/qmv_model.cpp q81 path: q4_0 d*(dot*d8 - 8*s8),
-// q8_0 d*d8*dot). Where the dot4 path re-reads every activation column for every weight row, here one wave
+// q8_0 d*d8*dot, q4_K d8*(d*sc*dot - dmin*mn*isum) per 32-element sub-block). Where the dot4 path re-reads every
+// activation column for every weight row, here one wave
 // serves 16 rows per activation read, which is what makes many columns cheap (used from 9 columns, and from 5-7
 // on rows longer than 8192).
 //
@@ -13,8 +14,9 @@
 // 4 (l / 16) .. + 3 of column l % 16. A = weights, B = activation, so a lane's four results share its own
 // activation column (one scale load) and need the weight scales of four rows (read from the staged rows in LDS).
 //
-// Work-group: 16 weight rows, 8 waves (up to 8192 rows) or 4, each over a contiguous share of the K blocks, 16
-// (q4_0) or 8 (q8_0) blocks per step staged through the wave's own LDS area with the next step's loads in flight; the partial
+// Work-group: 16 weight rows, 8 waves (up to 8192 rows) or 4, each over a contiguous share of the K blocks, 8
+// blocks per step (one super-block for q4_K) staged through the wave's own LDS area with the next step's loads in
+// flight; the partial
 // 16 x 16 tiles are added in LDS in a fixed order (deterministic, no workspace). Grid: ceil(M / 16).
 #include <type_traits>
 
@@ -26,8 +28,9 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-// Per weight type: block bytes and the per-block FP32 scaling of the integer block sum (the dot4 path's
-// arithmetic, so both forms round alike; only the order of the block sums differs).
+// Per weight type: bytes per 32-element block and the per-block FP32 scaling of the integer block sum (the dot4
+// path's arithmetic for the legacy types, so both forms round alike; only the order of the block sums differs).
+// dw / dm: the block's scale and (q4_K) min factor of the weight row, decoded once per step.
 template <int TYPE>
 struct MfmaW;
 
@@ -36,7 +39,8 @@ struct MfmaW;
 template <>
 struct MfmaW<Q4_0> {
     static constexpr int kBytes = 18;
-    static __device__ __forceinline__ float acc(float dw, int dot, float4 xs, float a) {
+    static constexpr bool kMins = false;
+    static __device__ __forceinline__ float acc(float dw, float, int dot, float4 xs, float a) {
         return fmaf(dw, fmaf(float(dot), xs.x, -8.0f * xs.y), a);
     }
 };
@@ -45,8 +49,22 @@ struct MfmaW<Q4_0> {
 template <>
 struct MfmaW<Q8_0> {
     static constexpr int kBytes = 34;
-    static __device__ __forceinline__ float acc(float dw, int dot, float4 xs, float a) {
+    static constexpr bool kMins = false;
+    static __device__ __forceinline__ float acc(float dw, float, int dot, float4 xs, float a) {
         return fmaf(dw * xs.x, float(dot), a);
+    }
+};
+
+// q4_K: 144-byte super-block {fp16 d, fp16 dmin, scales[12], qs[128]} of eight 32-element sub-blocks (18 bytes
+// per block on average; a step is one super-block). Sub-block j takes the low (j even) or high nibbles of
+// qs[32 (j / 2) ..] unsigned, with dw = d * sc_j and dm = dmin * mn_j: acc + d8 * (dw * dot - dm * isum), the
+// reference's d * (d8 * dot * sc) - dmin * (d8 * isum * mn) (UnitQ4_K::acc) regrouped per sub-block.
+template <>
+struct MfmaW<Q4_K> {
+    static constexpr int kBytes = 18;
+    static constexpr bool kMins = true;
+    static __device__ __forceinline__ float acc(float dw, float dm, int dot, float4 xs, float a) {
+        return fmaf(xs.x, fmaf(dw, float(dot), -dm * xs.z), a);
     }
 };
 
@@ -57,7 +75,7 @@ struct MfmaW<Q8_0> {
 #define P1X_MMQ_STEP_Q4_0 8  // K blocks per step (staged through LDS) for q4_0 (16: slower); q8_0 takes 8
 #endif
 template <int TYPE>
-constexpr int step_blocks() { return TYPE == Q4_0 ? P1X_MMQ_STEP_Q4_0 : 8; }
+constexpr int step_blocks() { return TYPE == Q4_0 ? P1X_MMQ_STEP_Q4_0 : 8; }  // q4_K: one super-block
 #ifndef P1X_MMQ_PF
 #define P1X_MMQ_PF 1  // steps whose loads are in flight per wave (1 or 2; 2 measured slower)
 #endif
@@ -80,12 +98,13 @@ constexpr uint32_t kOob = 0x7ffffff0u;
 // 16-byte loads per row: 320 bytes for 16 q4_0 blocks, 320 for 8 q8_0 blocks, each covering the step's blocks plus
 // the 2-byte alignment shift), the 16 activation columns' U blocks as [block][column][32 bytes] (the MFMA B-operand
 // reads are then 512 contiguous bytes per block), and their Q8_1 scales [block][column].
-template <int ROWDW, int U, int BC>
+template <int ROWDW, int U, int BC, bool MINS>
 struct MmqStage {
     uint32_t w[16][ROWDW];
     uint32_t a[U][BC][8];
     float4 s[U][BC];
-    float dw[U][16];  // the weight scales of the step, decoded once per (block, row)
+    float dw[U][16];             // the weight scales of the step, decoded once per (block, row)
+    float dm[MINS ? U : 1][16];  // and (q4_K) the min factors
 };
 
 // NW waves per work-group, each over a contiguous share of the K blocks: 8 where the grid is small (M <= 8192, at
@@ -107,6 +126,7 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
     constexpr int BB = W::kBytes;
     constexpr int NWL = (U * BB + 4 + 63) / 64;  // 16-byte loads per lane (4 lanes per row)
     static_assert(!ALN || (U * BB) % 16 == 0, "aligned steps are whole 16-byte chunks");
+    static_assert(TYPE != Q4_K || (ALN && U == 8), "q4_K: aligned rows, one super-block per step");
     constexpr int NCH = ALN ? U * BB / 16 : 4 * NWL;      // 16-byte chunks staged per row and step
     constexpr int NLD = ALN ? (16 * NCH + 63) / 64 : NWL;  // weight loads per lane
     // Staged dwords per row. Padding spreads the 16 rows over LDS banks: aligned rows take a stride of 4 x an odd
@@ -114,7 +134,7 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
     constexpr int ROWDW = ALN ? 4 * (NCH | 1) : 4 * NCH + P1X_MMQ_PAD;
     static_assert(BC == 8 || BC == 16, "8 or 16 staged columns");
     constexpr int NA = U * BC / 32, NS = U * BC / 64;  // activation and scale loads per lane (BC columns x U blocks)
-    __shared__ MmqStage<ROWDW, U, BC> stage[NW];
+    __shared__ MmqStage<ROWDW, U, BC, W::kMins> stage[NW];
     __shared__ float red[NW - 1][4][64];  // partial tiles of waves 1.., result-major (conflict-free)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, i16 = lane & 15;
@@ -122,7 +142,7 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
     const int nblk = K / 32;
     const int per = ALN ? (nblk + NW * U - 1) / (NW * U) * U : (nblk + NW - 1) / NW;
     const int b0 = min(nblk, wave * per), b1 = min(nblk, b0 + per);
-    MmqStage<ROWDW, U, BC>& st = stage[wave];
+    MmqStage<ROWDW, U, BC, W::kMins>& st = stage[wave];
 
     // Global side of the staging: lane (row lane/4, quarter lane%4) reads NWL x 16 bytes of its row's dword-aligned
     // span.
@@ -212,6 +232,11 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
             bytes_at(i16, sh + u * BB + 2 + 8 * (g & 1), q2, 2);
             const uint32_t shn = (g & 2) ? 4u : 0u;
             wa = long((q2[0] >> shn) & 0x0F0F0F0Fu) | (long((q2[1] >> shn) & 0x0F0F0F0Fu) << 32);
+        } else if constexpr (TYPE == Q4_K) {
+            // qs bytes 32 (u / 2) + 8g .. + 7 (super-block bytes 16 + ..., 8-byte aligned), nibble u % 2.
+            const uint2 q2 = *reinterpret_cast<const uint2*>(&st.w[i16][4 + 8 * (u >> 1) + 2 * g]);
+            const uint32_t shn = 4u * (u & 1);
+            wa = long((q2.x >> shn) & 0x0F0F0F0Fu) | (long((q2.y >> shn) & 0x0F0F0F0Fu) << 32);
         } else {
             uint32_t q2[2];
             bytes_at(i16, sh + u * BB + 2 + 8 * g, q2, 2);
@@ -223,9 +248,14 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
         const v4i dd = __builtin_amdgcn_mfma_i32_16x16x32_i8(wa, xa, zero, 0, 0, 0);
         const float4 dw4 = *reinterpret_cast<const float4*>(&st.dw[u][4 * g]);
         const float dw[4] = {dw4.x, dw4.y, dw4.z, dw4.w};
+        float dm[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (W::kMins) {
+            const float4 dm4 = *reinterpret_cast<const float4*>(&st.dm[u][4 * g]);
+            dm[0] = dm4.x, dm[1] = dm4.y, dm[2] = dm4.z, dm[3] = dm4.w;
+        }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float v = W::acc(dw[r], dd[r], xs, acc[r]);
+            const float v = W::acc(dw[r], dm[r], dd[r], xs, acc[r]);
             acc[r] = ok ? v : acc[r];
             if (SUMS) {
                 const int m = m0 + 4 * g + r;
@@ -250,7 +280,15 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
 #pragma unroll
         for (int k = 0; k < U / 4; ++k) {
             const int row = lane & 15, u = (lane >> 4) + 4 * k;
-            st.dw[u][row] = half_bits_to_float(u16_at(row, row_shift(row, bs) + u * BB));
+            if constexpr (TYPE == Q4_K) {
+                const uint32_t h = st.w[row][0];  // fp16 d, fp16 dmin
+                int sc, mn;
+                q4k_scale_min(st.w[row][1], st.w[row][2], st.w[row][3], u, sc, mn);
+                st.dw[u][row] = half_bits_to_float(h) * float(sc);
+                st.dm[u][row] = half_bits_to_float(h >> 16) * float(mn);
+            } else {
+                st.dw[u][row] = half_bits_to_float(u16_at(row, row_shift(row, bs) + u * BB));
+            }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -318,11 +356,14 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
 #define P1X_MMQ_MIN_COLS 9  // columns from which the matrix-core form replaces the dot4 kernels
 #endif
 
-bool mmq_supported(int type, int B) { return (type == Q4_0 || type == Q8_0) && B >= 1 && B <= kMmqMaxCols; }
-// The staging loads address the weight matrix through one 32-bit buffer range.
-bool mmq_fits(int M, int64_t nb01, int K, int B) {
+bool mmq_supported(int type, int B) {
+    return (type == Q4_0 || type == Q8_0 || type == Q4_K) && B >= 1 && B <= kMmqMaxCols;
+}
+// The staging loads address the weight matrix through one 32-bit buffer range; q4_K stages whole 16-byte chunks
+// of its rows (a row stride of 16-byte multiples, as every unpadded q4_K row is).
+bool mmq_fits(int type, int M, int64_t nb01, int K, int B) {
     return int64_t(M) * nb01 + 3 <= int64_t(kOob) && int64_t(B) * K <= int64_t(kOob) &&
-           int64_t(B) * (K / 32) * 16 <= int64_t(kOob);
+           int64_t(B) * (K / 32) * 16 <= int64_t(kOob) && (type != Q4_K || nb01 % 16 == 0);
 }
 // From 9 columns always. Below that, measured per shape (graph period of the kernel on a prepared activation,
 // dot4 against the matrix-core form): rows longer than 8192 on at most 8192 rows from 5 columns, where the dot4
@@ -333,9 +374,26 @@ bool mmq_fits(int M, int64_t nb01, int K, int B) {
 // 6.2 / 6.7 / 7.5 against 6.6 / 6.7 / 6.8; q8_0 14336x4096 18.2 / 19.8 / 24.7 against 19.7 / 19.9 / 20.3,
 // 4096x4096 7.4 / 7.7 / 9.3 against 7.6 / 7.7 / 8.0 us); fewer rows stay on dot4 (1024x4096 at 8 columns 3.8 against
 // 5.9 us).
+// q4_K, whose dot4 kernels slow down steeply with the column count (two Q8_1 blocks and their scale / min codes
+// per 64-element unit), measured the same way (dot4 against the matrix cores, 1 / 2 / 3 / 8 columns):
+// 4096x14336 9.8 / 13.4 / 16.6 / 85.8 against 13.1 / 13.1 / 13.4 / 14.1 us, 14336x4096 8.9 / 11.2 / 16.1 / 42.1
+// against 14.1 / 14.8 / 14.6 / 15.8, 4096x4096 4.6 / 5.3 / 6.7 / 13.9 against 6.3 / 6.2 / 6.3 / 6.4, 1024x4096
+// 3.1 / 3.4 / 3.9 / 5.8 against 5.3 / 5.3 / 5.4 / 5.6 (the h16 path: 16.7 / 25.5 / 28.5 / 79.2 at 4096x14336).
+#ifndef P1X_MMQ_MIN_COLS_Q4_K_LONG
+#define P1X_MMQ_MIN_COLS_Q4_K_LONG 2  // q4_K rows longer than 8192, at least 4096 rows
+#endif
+#ifndef P1X_MMQ_MIN_COLS_Q4_K
+#define P1X_MMQ_MIN_COLS_Q4_K 3  // q4_K rows of at most 8192, at least 4096 rows
+#endif
+#ifndef P1X_MMQ_MIN_COLS_Q4_K_FEW_ROWS
+#define P1X_MMQ_MIN_COLS_Q4_K_FEW_ROWS 8  // q4_K, fewer than 4096 rows
+#endif
 bool mmq_preferred(int type, int B, int M, int K) {
     if (!mmq_supported(type, B)) return false;
     if (B >= P1X_MMQ_MIN_COLS) return true;
+    if (type == Q4_K)
+        return M >= 4096 ? B >= (K > 8192 ? P1X_MMQ_MIN_COLS_Q4_K_LONG : P1X_MMQ_MIN_COLS_Q4_K)
+                         : B >= P1X_MMQ_MIN_COLS_Q4_K_FEW_ROWS;
     if (K > 8192) return M <= 8192 && B >= (type == Q8_0 ? P1X_MMQ_MIN_COLS_LONG_Q8_0 : P1X_MMQ_MIN_COLS_LONG_Q4_0);
     return M >= 4096 && B >= P1X_MMQ_MIN_COLS_SHORT;
 }
@@ -372,6 +430,10 @@ hipError_t launch_mmq(int type, int B, const void* w, int64_t nb01, int M, int K
     } else if (type == Q8_0) {
         if (gs) P1X_MMQ(Q8_0, true);
         else P1X_MMQ(Q8_0, false);
+    } else if (type == Q4_K && nb01 % 16 == 0) {
+        // Rows of whole 16-byte chunks from a 4-byte aligned base: the 16-byte buffer loads need dword alignment.
+        if (gs) P1X_MMQ_L(Q4_K, true, true);
+        else P1X_MMQ_L(Q4_K, false, true);
     } else {
         return hipErrorInvalidValue;
     }

@@ -187,18 +187,7 @@ struct UnitQ8_0 {
 
 // q4_K: 144-byte super-block {fp16 d, fp16 dmin, scales[12], qs[128]}; a unit is the pair of sub-blocks
 // 2g, 2g+1 that share qs[32g..32g+31] (low / high nibbles). Six-bit scale/min codes as get_scale_min_k4
-// (qmv_model.cpp:72-77). Value = d*sc*q - dmin*mn; Q8_1 terms d8*dot*sc and d8*isum*mn (qmv_model.cpp:166-178).
-__device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j, int& sc, int& mn) {
-    const int sh = 8 * (j & 3);
-    const uint32_t b0 = (s0 >> sh) & 255, b1 = (s1 >> sh) & 255, b2 = (s2 >> sh) & 255;
-    if (j < 4) {
-        sc = int(b0 & 63);
-        mn = int(b1 & 63);
-    } else {
-        sc = int((b2 & 15) | ((b0 >> 6) << 4));
-        mn = int((b2 >> 4) | ((b1 >> 6) << 4));
-    }
-}
+// (q4k_scale_min). Value = d*sc*q - dmin*mn; Q8_1 terms d8*dot*sc and d8*isum*mn (qmv_model.cpp:166-178).
 struct UnitQ4_K {
     static constexpr int kElems = 64, kGroups = 2, kActBlocks = 2;
     uint32_t hdr[4], q[8];

@@ -126,8 +126,8 @@ def _predicate_in_subprocess(env):
 
     code = ("import ctypes as C, p100_amd as P; f = P.load_symbols_only()['p1x_should_use_mmvh']; "
             "f.restype = C.c_int; f.argtypes = [C.c_int, C.c_int64, C.c_int64, C.c_int64]; "
-            "print([f(12, 4096, 14336, 4), f(12, 4096, 4096, 4), f(2, 4096, 4096, 1), f(2, 4096, 4096, 9), "
-            "f(3, 64, 64, 1)])")
+            "print([f(12, 1024, 14336, 4), f(12, 4096, 4096, 4), f(2, 4096, 4096, 1), f(2, 4096, 4096, 9), "
+            "f(3, 64, 64, 1), f(12, 4096, 14336, 4)])")
     e = {k: v for k, v in os.environ.items() if k not in ("P1X_FORCE_MMVH", "P1X_DISABLE_MMVH")}
     e.update(env)
     out = subprocess.run([sys.executable, "-c", code], env=e, capture_output=True, text=True, check=True,
@@ -137,12 +137,13 @@ def _predicate_in_subprocess(env):
 
 def test_should_use_mmvh_and_overrides():
     """The selection predicate (the counterpart of ggml_cuda_should_use_mmvh, 0005 patch :344-352): q4_K rows longer
-    than 8192 at 4..8 columns prefer h16; FORCE selects h16 for every supported shape (ncols 1..8, known type);
-    DISABLE turns the preference off; FORCE wins over DISABLE, as in the reference."""
-    assert _predicate_in_subprocess({}) == [1, 0, 0, 0, 0]
-    assert _predicate_in_subprocess({"P1X_DISABLE_MMVH": "1"}) == [0, 0, 0, 0, 0]
-    assert _predicate_in_subprocess({"P1X_FORCE_MMVH": "1"}) == [1, 1, 1, 0, 0]
-    assert _predicate_in_subprocess({"P1X_FORCE_MMVH": "1", "P1X_DISABLE_MMVH": "1"}) == [1, 1, 1, 0, 0]
+    than 8192 at 4..8 columns prefer h16 where the int8 matrix-core form does not take them (fewer than 4096 rows);
+    FORCE selects h16 for every supported shape (ncols 1..8, known type); DISABLE turns the preference off; FORCE
+    wins over DISABLE, as in the reference."""
+    assert _predicate_in_subprocess({}) == [1, 0, 0, 0, 0, 0]
+    assert _predicate_in_subprocess({"P1X_DISABLE_MMVH": "1"}) == [0, 0, 0, 0, 0, 0]
+    assert _predicate_in_subprocess({"P1X_FORCE_MMVH": "1"}) == [1, 1, 1, 0, 0, 1]
+    assert _predicate_in_subprocess({"P1X_FORCE_MMVH": "1", "P1X_DISABLE_MMVH": "1"}) == [1, 1, 1, 0, 0, 1]
 
 
 def test_fa_kernel_selection_and_plan_bounds_without_gpu():

@@ -178,6 +178,75 @@ def test_many_columns_parity(orc, gpu, tname):
             assert (y3.view(np.uint32) == y2.view(np.uint32)).all()
 
 
+def _q4_k_case(orc, t, w, x, rows, k, nb01=None, offset=0):
+    """q4_K through the fp32 op (with and without group sums) and a prepared activation, the weights at nb01 bytes
+    per row from byte `offset` of a device buffer: sums bit-exact, FP32 within the bars, the fp32 op's two calls alike
+    bit for bit, and the prepared activation's too on the matrix cores (9..16 columns; at 1..8 the fp32 op may take
+    the single-launch dot4 kernel, whose FP32 sums are grouped differently)."""
+    import p100_amd as P
+
+    torch = _torch()
+    rb = w.shape[1]
+    nb01 = nb01 or rb
+    buf = np.zeros(offset + rows * nb01, np.uint8)
+    buf[offset:].reshape(rows, nb01)[:, :rb] = w
+    dev = to_dev(buf)
+    wd = dev[offset:]
+    assert wd.data_ptr() % 16 == offset % 16
+    y, sums = P.mul_mat_vec(t, wd, rows, k, to_dev(x), act="q8_1", nb01=nb01, group_sums=True)
+    check_matvec(orc, t, w, x, y.cpu().numpy(), sums.cpu().numpy(), "q81")
+    y2 = P.mul_mat_vec(t, wd, rows, k, to_dev(x), act="q8_1", nb01=nb01).cpu().numpy()
+    y3 = P.mul_mat_vec(t, wd, rows, k, P.quantize_q8_1(to_dev(x)), nb01=nb01).cpu().numpy()
+    assert (y2.view(np.uint32) == y.cpu().numpy().view(np.uint32)).all()
+    if x.shape[0] > 8:
+        assert (y3.view(np.uint32) == y2.view(np.uint32)).all()
+    else:
+        check_matvec(orc, t, w, x, y3, None, "q81")
+    torch.cuda.synchronize()
+
+
+def test_q4_K_many_columns(orc, gpu):
+    """q4_K at 9..16 columns (the int8 matrix-core form, one 144-byte super-block per step and wave): eight
+    32-element sub-blocks per step with their six-bit scale / min codes, low and high nibbles of the shared quant
+    bytes. One and two super-blocks per row (idle waves in the K split), partial 16-row tiles, the full-size
+    shapes, past 8192 rows (4 waves per work-group), a 4-byte (not 16-byte) aligned base, and a padded row stride
+    of 16-byte multiples."""
+    t = orc.TYPES["q4_K"]
+    for k, rows in ((256, 17), (512, 16), (256, 33), (4096, 17), (14336, 33), (4096, 4096), (256, 8200)):
+        for ncols in ((9, 12, 16) if rows < 4096 else (16,)):
+            w, x = make_case(orc, t, k, rows, ncols, seed=3100 + k + rows + ncols)
+            _q4_k_case(orc, t, w, x, rows, k)
+    w, x = make_case(orc, t, 512, 19, 12, seed=3201)
+    _q4_k_case(orc, t, w, x, 19, 512, offset=4)
+    _q4_k_case(orc, t, w, x, 19, 512, nb01=w.shape[1] + 16, offset=8)
+
+
+def test_q4_K_few_columns_matrix_cores(orc, gpu):
+    """q4_K at 2..8 columns where the matrix-core form takes the shape (from 2 columns on rows longer than 8192,
+    from 3 on at least 4096 rows, at 8 on fewer rows): 8 staged activation columns, 8 waves per work-group up to
+    8192 rows and 4 beyond, partial last row tiles; sums bit-exact, FP32 within the bars."""
+    t = orc.TYPES["q4_K"]
+    for k, rows, ncols in ((8448, 4100, 2), (8448, 4100, 5), (256, 4104, 3), (256, 4104, 8), (256, 8200, 3),
+                           (1024, 40, 8)):
+        w, x = make_case(orc, t, k, rows, ncols, seed=3400 + k + rows + ncols)
+        _q4_k_case(orc, t, w, x, rows, k)
+
+
+def test_q4_K_many_columns_unaligned_stride(orc, gpu):
+    """A q4_K row stride that is not a multiple of 16 bytes cannot take the matrix-core staging: 9..16 columns
+    are refused with EUNSUPPORTED, 1..8 columns run the dot4 kernels."""
+    import p100_amd as P
+
+    t = orc.TYPES["q4_K"]
+    w, x = make_case(orc, t, 512, 17, 9, seed=3301)
+    rb = w.shape[1]
+    pad = np.zeros((17, rb + 4), np.uint8)
+    pad[:, :rb] = w
+    with pytest.raises(P.P1XError, match="16-byte"):
+        P.mul_mat_vec(t, to_dev(pad), 17, 512, to_dev(x), nb01=rb + 4)
+    _q4_k_case(orc, t, w, x[:8], 17, 512, nb01=rb + 4)
+
+
 @pytest.mark.parametrize("tname", ["q4_0", "q8_0"])
 def test_long_rows_five_to_eight_columns(orc, gpu, tname):
     """Rows longer than 8192 at 5-8 columns (the matrix-core form with 8 staged activation columns, dot4 below 5
@@ -342,8 +411,10 @@ def test_invalid_arguments(gpu):
         P.mul_mat_vec("q4_K", w, 1, 32, x)
     with pytest.raises(ValueError, match="ncols"):
         P.mul_mat_vec("q4_0", w, 1, 32, torch.zeros((17, 32), device="cuda"))
-    with pytest.raises(ValueError, match="ncols"):  # 9..16 columns: q4_0 / q8_0 with a Q8_1 activation only
+    with pytest.raises(ValueError, match="ncols"):  # 9..16 columns: q4_0 / q8_0 / q4_K with a Q8_1 activation only
         P.mul_mat_vec("q4_0", w, 1, 32, torch.zeros((9, 32), device="cuda"), act="h16")
+    with pytest.raises(ValueError, match="ncols"):
+        P.mul_mat_vec("q6_K", w, 1, 256, torch.zeros((9, 256), device="cuda"))
     with pytest.raises(ValueError, match="row stride"):
         P.mul_mat_vec("q4_0", w, 1, 32, x, nb01=16)
     with pytest.raises(P.P1XError):
