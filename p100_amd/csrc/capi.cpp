@@ -247,7 +247,7 @@ size_t p1x_mul_mat_vec_workspace(int wtype, int64_t M, int64_t K, int64_t ncols,
     // 5.7 -> 4.6 us, 4096x4096 unchanged).
     const bool fused = K <= INT32_MAX && M <= INT32_MAX &&
                        !p1x::mmq_preferred(wtype, int(ncols), int(M), int(K)) &&
-                       p1x::mmvq_fused_fits(int(ncols), int(M), int(K));
+                       p1x::mmvq_fused_fits(wtype, int(ncols), int(M), int(K));
     return fused ? 0 : q8_1_bytes(K, ncols);
 }
 

@@ -225,7 +225,7 @@ int p1x_llama_decode_step(const p1x_llama_model* m, p1x_decode_state* state, con
         fa.oq = qs;
         fa.ods = reinterpret_cast<float4*>(ds);
     }
-    const bool wo_fused = !wo_prepared && p1x::mmvq_fused_fits(1, E, E);
+    const bool wo_fused = !wo_prepared && p1x::mmvq_fused_fits(hp.wtype, 1, E, E);
     // RoPE and the KV append ride on the q/k/v projection when its register-resident kernel applies to every
     // part of the stack (q rows and k / v rows), else they take their own launch.
     const bool rope_fused = p1x::mmvq_rope_kv_supported(hp.wtype, E + 2 * kv, E, d) &&

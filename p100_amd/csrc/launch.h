@@ -25,7 +25,7 @@ hipError_t launch_read_bytes(const void* src, int64_t bytes, uint32_t* digest, i
 // rejected). Else xq/xds hold a prepared Q8_1 activation.
 hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
                        const float* x, float* y, int32_t* gs, hipStream_t stream);
-bool mmvq_fused_fits(int B, int M, int K);
+bool mmvq_fused_fits(int type, int B, int M, int K);
 // The batched (ggml broadcast) mat-vec on a prepared Q8_1 activation of B * ne12 * ne13 columns: the streaming kernel
 // with one slice per grid (y, z) position.
 hipError_t launch_mmvq_batched(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq,

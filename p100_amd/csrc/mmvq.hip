@@ -55,6 +55,9 @@
 #ifndef P1X_MMVR_ENABLE
 #define P1X_MMVR_ENABLE 1  // one prepared q4_0 / q8_0 column: register-resident activation kernel (k_mmvr)
 #endif
+#ifndef P1X_MMVR_FUSED
+#define P1X_MMVR_FUSED 1  // one f32 q4_0 / q8_0 column in one launch: k_mmvr quantizing x per work-group
+#endif
 
 namespace p1x {
 namespace {
@@ -475,16 +478,20 @@ __global__ __launch_bounds__(256) void k_mmvq_fx(const uint8_t* __restrict__ w, 
 // (that kernel's 64*ceil(K/512) threads in one pass map to threads t + 256 i, i < NV, here): lane sums of squares
 // over 8 consecutive elements, the same wave sum, the wave totals added in order, rsqrt(mean + eps), (x * scale) *
 // w, Q8_1 by quads. The blocks are therefore bit-identical to that kernel's and go through LDS to their owners.
+// SrcNorm<NV, false>: x itself quantized the same way (k_quantize_q8_1's quads, bit-identical blocks): the whole
+// mat-vec op from an f32 activation in one launch, with the weight stream requested before the quantization.
 struct SrcQ81 {
     static constexpr int kNV = 0;
+    static constexpr bool kNorm = false;
     const int8_t* xq;
     const float4* xds;
 };
-template <int NV>
+template <int NV, bool NORM = true>
 struct SrcNorm {
     static constexpr int kNV = NV;  // 8-element chunks per thread: K <= 2048 * NV
+    static constexpr bool kNorm = NORM;
     const float* x;
-    const float* w;
+    const float* w;  // NORM only
     float eps;
 };
 template <int NV>
@@ -504,48 +511,55 @@ template <>
 struct NormIn<0> {};
 // Chunk i of thread t: elements 8 (t + 256 i) .. + 7; a chunk past K is read at K - 8 and zeroed (no branch, so
 // the weight loads issued next stay in flight).
-template <int NV>
-__device__ __forceinline__ NormIn<NV> norm_load(const SrcNorm<NV>& src, int K) {
+template <int NV, bool NORM>
+__device__ __forceinline__ NormIn<NV> norm_load(const SrcNorm<NV, NORM>& src, int K) {
     NormIn<NV> in;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int e0 = 8 * (int(threadIdx.x) + 256 * i), ec = e0 < K ? e0 : K - 8;
         const float4* xp = reinterpret_cast<const float4*>(src.x + ec);
-        const float4* wp = reinterpret_cast<const float4*>(src.w + ec);
-        const float4 x0 = xp[0], x1 = xp[1], w0 = wp[0], w1 = wp[1];
+        const float4 x0 = xp[0], x1 = xp[1];
         const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-        const float ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            in.x[i][e] = e0 < K ? xs[e] : 0.0f;
-            in.w[i][e] = ws[e];
+        for (int e = 0; e < 8; ++e) in.x[i][e] = e0 < K ? xs[e] : 0.0f;
+        if constexpr (NORM) {
+            const float4* wp = reinterpret_cast<const float4*>(src.w + ec);
+            const float4 w0 = wp[0], w1 = wp[1];
+            const float ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) in.w[i][e] = ws[e];
         }
     }
     return in;
 }
-// RMSNorm + Q8_1 of the loaded chunks into LDS (two work-group barriers); every thread of the work-group calls it.
-template <int NV>
+// RMSNorm (NORM) + Q8_1 of the loaded chunks into LDS (two work-group barriers, one without the norm); every thread
+// of the work-group calls it.
+template <bool NORM, int NV>
 __device__ __forceinline__ void norm_q8_1_to_lds(const NormIn<NV>& in, int K, float eps, NormLds<NV>& l) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nwv = (K / 8 + 63) / 64;  // waves of the standalone kernel (one pass)
+    const int tid = threadIdx.x;
+    float scale = 1.0f;
+    if constexpr (NORM) {
+        const int lane = tid & 63, wave = tid >> 6;
+        const int nwv = (K / 8 + 63) / 64;  // waves of the standalone kernel (one pass)
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        float ss = 0.0f;
+        for (int i = 0; i < NV; ++i) {
+            float ss = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) ss = fmaf(in.x[i][e], in.x[i][e], ss);
-        ss = norm_wave_total(ss);
-        if (lane == 0 && wave + 4 * i < nwv) l.part[wave + 4 * i] = ss;
+            for (int e = 0; e < 8; ++e) ss = fmaf(in.x[i][e], in.x[i][e], ss);
+            ss = norm_wave_total(ss);
+            if (lane == 0 && wave + 4 * i < nwv) l.part[wave + 4 * i] = ss;
+        }
+        __syncthreads();
+        float tot = 0.0f;
+        for (int k = 0; k < nwv; ++k) tot += l.part[k];
+        scale = rsqrtf(tot / float(K) + eps);
     }
-    __syncthreads();
-    float tot = 0.0f;
-    for (int k = 0; k < nwv; ++k) tot += l.part[k];
-    const float scale = rsqrtf(tot / float(K) + eps);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int vl = tid + 256 * i;
         float hv[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) hv[e] = (in.x[i][e] * scale) * in.w[i][e];
+        for (int e = 0; e < 8; ++e) hv[e] = NORM ? (in.x[i][e] * scale) * in.w[i][e] : in.x[i][e];
         const Q81Quad r = q8_1_quad(hv);
         if (8 * vl < K) {
             const int b = vl >> 2, qd = vl & 3;
@@ -691,7 +705,7 @@ __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int
     const auto est = epi.template prepare<R>(epi_in, row0, M);
     if constexpr (NV > 0) {  // the weight stream stays in flight across the barriers (they wait for LDS only)
         __shared__ NormLds<NV> nl;
-        norm_q8_1_to_lds(nin, K, src.eps, nl);
+        norm_q8_1_to_lds<SRC::kNorm>(nin, K, src.eps, nl);
         const ActLds al{nl.lo, nl.hi, nl.ds, units};
 #pragma unroll
         for (int j = 0; j < UPT; ++j) x[j] = al.get(0, uc[j]);
@@ -773,7 +787,7 @@ hipError_t launch_mmvr(const MmvrPlan& p, const uint8_t* w, int64_t nb01, int M,
 #define P1X_MMVR(NW, UP, RR)                                                                                        \
     if (p.nwk == NW && p.upt == UP && p.r == RR) {                                                                 \
         const dim3 grid((M + (4 / NW) * RR - 1) / ((4 / NW) * RR));                                                \
-        if constexpr (SRC::kNV == 0) {                                                                             \
+        if constexpr (SRC::kNV == 0 || !SRC::kNorm) {                                                              \
             if (gs) {                                                                                              \
                 hipLaunchKernelGGL((k_mmvr<TYPE, NW, UP, RR, true, EPI, SRC>), grid, dim3(256), 0, stream, w, nb01, M, \
                                    K, src, epi, gs);                                                               \
@@ -1026,12 +1040,19 @@ int mmvq_type_rows_per_wave(int type, int M, int B, bool fused) {
 // The single-launch form (x quantized into LDS by each work-group), for one column, when its 48 bytes per block
 // fit in 64 KiB of LDS and the repeated quantization (work-groups x K elements) stays small next to the weight
 // stream; otherwise the activation goes through p1x_quantize_q8_1 and a workspace.
-bool mmvq_fused_fits(int B, int M, int K) {
+bool mmvr_norm_plan(int type, int M, int K, MmvrPlan& p);
+bool mmvq_fused_fits(int type, int B, int M, int K) {
     if (B != 1) return false;
-    const int rw = mmvq_rows_per_wave(M, B, true);
-    const long wgs = (M + 4L * rw - 1) / (4L * rw);  // every work-group quantizes all B x K elements
+    MmvrPlan plan;
+    const bool mmvr = P1X_MMVR_FUSED && mmvr_norm_plan(type, M, K, plan);
+    const int rows = mmvr ? (4 / plan.nwk) * plan.r : 4 * mmvq_rows_per_wave(M, B, true);
+    const long wgs = (M + rows - 1L) / rows;  // every work-group quantizes all B x K elements
     return size_t(48) * B * (K / 32) <= 65536 && wgs * K * B <= P1X_MMVQ_FUSE_MAX;
 }
+
+template <int TYPE>
+hipError_t launch_mmvr_f32(const MmvrPlan& p, const uint8_t* w, int64_t nb01, int M, int K, const float* x, float* y,
+                           int32_t* gs, hipStream_t stream);
 
 hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
                        const float* x, float* y, int32_t* gs, hipStream_t stream) {
@@ -1045,6 +1066,9 @@ hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int 
     if (B == 1 && !x && P1X_MMVR_ENABLE && (type == Q4_0 || type == Q8_0) && mmvr_plan(type, M, K, plan))
         return type == Q4_0 ? launch_mmvr<Q4_0>(plan, wb, nb01, M, K, SrcQ81{xq, d4}, EpiRows{y, nullptr}, gs, stream)
                             : launch_mmvr<Q8_0>(plan, wb, nb01, M, K, SrcQ81{xq, d4}, EpiRows{y, nullptr}, gs, stream);
+    if (B == 1 && x && P1X_MMVR_FUSED && (type == Q4_0 || type == Q8_0) && mmvr_norm_plan(type, M, K, plan))
+        return type == Q4_0 ? launch_mmvr_f32<Q4_0>(plan, wb, nb01, M, K, x, y, gs, stream)
+                            : launch_mmvr_f32<Q8_0>(plan, wb, nb01, M, K, x, y, gs, stream);
     switch (type) {
         case Q4_0: return launch_type<Q4_0>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
         case Q8_0: return launch_type<Q8_0>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
@@ -1083,6 +1107,17 @@ hipError_t launch_mmvr_norm(const MmvrPlan& p, const uint8_t* w, int64_t nb01, i
     if (units <= 64) return launch_mmvr<TYPE>(p, w, nb01, M, K, SrcNorm<1>{n.x, n.w, n.eps}, epi, nullptr, stream);
     if (units <= 128) return launch_mmvr<TYPE>(p, w, nb01, M, K, SrcNorm<2>{n.x, n.w, n.eps}, epi, nullptr, stream);
     return launch_mmvr<TYPE>(p, w, nb01, M, K, SrcNorm<4>{n.x, n.w, n.eps}, epi, nullptr, stream);
+}
+
+// The whole op from an f32 activation column in one launch (the work-group quantizes x, as k_quantize_q8_1 does).
+template <int TYPE>
+hipError_t launch_mmvr_f32(const MmvrPlan& p, const uint8_t* w, int64_t nb01, int M, int K, const float* x, float* y,
+                           int32_t* gs, hipStream_t stream) {
+    const int units = K / 32;
+    const EpiRows epi{y, nullptr};
+    if (units <= 64) return launch_mmvr<TYPE>(p, w, nb01, M, K, SrcNorm<1, false>{x, nullptr, 0.0f}, epi, gs, stream);
+    if (units <= 128) return launch_mmvr<TYPE>(p, w, nb01, M, K, SrcNorm<2, false>{x, nullptr, 0.0f}, epi, gs, stream);
+    return launch_mmvr<TYPE>(p, w, nb01, M, K, SrcNorm<4, false>{x, nullptr, 0.0f}, epi, gs, stream);
 }
 
 bool mmvq_norm_supported(int type, int M, int K) {
