@@ -82,6 +82,9 @@ constexpr int step_blocks() { return TYPE == Q4_0 ? P1X_MMQ_STEP_Q4_0 : 8; }  //
 #ifndef P1X_MMQ_UNROLL
 #define P1X_MMQ_UNROLL 8  // blocks of a step unrolled together (more keeps too many operands live)
 #endif
+#ifndef P1X_MMQ_CLAMP
+#define P1X_MMQ_CLAMP 1  // loads of steps past the wave's share read nothing (range-checked offset)
+#endif
 
 // Buffer loads with a range check: offsets at or past the resource size read zeros and touch no memory, so the
 // staging loads past the matrix end, past the last activation column or in padded columns need no branch.
@@ -171,26 +174,28 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
     // Activation staging: piece p of the step (16 bytes) is (block p / 2BC, column p % 2BC / 2, half p % 2) and
     // scale entry p is (block p / BC, column p % BC), so a lane's LDS write lands at p x 16 bytes: consecutive
     // lanes, consecutive banks. (The global loads touch the same cache lines in any lane order.)
+    // A step past the share (the prefetch after the last one) reads nothing: its offsets are moved out of range.
     auto load = [&](int bs, auto slot_tag) {
         constexpr int S = decltype(slot_tag)::value;
+        const bool live = !P1X_MMQ_CLAMP || bs < b1;
         if constexpr (ALN) {
 #pragma unroll
             for (int k = 0; k < NLD; ++k)
-                rw[S][k] = ld16(wr, k * 64 + lane < 16 * NCH ? arow_off[k] + uint32_t(bs) * BB : kOob);
+                rw[S][k] = ld16(wr, k * 64 + lane < 16 * NCH && live ? arow_off[k] + uint32_t(bs) * BB : kOob);
         } else {
-            const uint32_t wb = (srow_off + uint32_t(bs) * BB) & ~3u;
+            const uint32_t wb = live ? (srow_off + uint32_t(bs) * BB) & ~3u : kOob;
 #pragma unroll
             for (int k = 0; k < NWL; ++k) rw[S][k] = ld16(wr, wb + (sq * NWL + k) * 16);
         }
 #pragma unroll
         for (int j = 0; j < NA; ++j) {
             const int p = j * 64 + lane, u = p / (2 * BC), c = (p >> 1) % BC;
-            ra[S][j] = ld16(xr, c < B ? uint32_t(c * K + (bs + u) * 32 + (p & 1) * 16) : kOob);
+            ra[S][j] = ld16(xr, c < B && live ? uint32_t(c * K + (bs + u) * 32 + (p & 1) * 16) : kOob);
         }
 #pragma unroll
         for (int j = 0; j < NS; ++j) {
             const int p = j * 64 + lane, u = p / BC, c = p % BC;
-            rs[S][j] = ld16(dr, c < B ? uint32_t((c * nblk + bs + u) * 16) : kOob);
+            rs[S][j] = ld16(dr, c < B && live ? uint32_t((c * nblk + bs + u) * 16) : kOob);
         }
     };
     auto store = [&](auto slot_tag) {
@@ -306,10 +311,11 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
     if (b0 < b1) {
         load(b0, I0{});
         if constexpr (PF == 2) load(b0 + U, I1{});
+        // Whole rounds of PF steps, no step behind a branch (a branch would wait for every load in flight): with
+        // an odd step count and PF = 2 the last round's second step lies past b1 and adds nothing.
         for (int bs = b0; bs < b1; bs += PF * U) {
             step(bs, I0{});
-            if constexpr (PF == 2)
-                if (bs + U < b1) step(bs + U, I1{});
+            if constexpr (PF == 2) step(bs + U, I1{});
         }
     }
 
