@@ -113,9 +113,9 @@ int p1x_quantize_q8_1(const float* x, int8_t* qs, float* ds, int64_t K, int64_t 
 int p1x_prepare_h16(const float* x, uint16_t* h, float* meta, int64_t K, int64_t ncols, void* stream);
 
 /*
- * y[c*M + m] = sum_k deq(w[m])[k] * x[c*K + k] for c < ncols, m < M. ncols (ne11) is 1..8, and 1..16 for q4_0 /
- * q8_0 / q4_K with P1X_ACT_Q8_1 (9..16 columns run on int8 matrix cores; the int32 block sums are the same; q4_K
- * there needs nb01 a multiple of 16, else P1X_EUNSUPPORTED).
+ * y[c*M + m] = sum_k deq(w[m])[k] * x[c*K + k] for c < ncols, m < M. ncols (ne11) is 1..8, and 1..16 with
+ * P1X_ACT_Q8_1 (9..16 columns run on int8 matrix cores; the int32 block sums are the same; q4_K there needs nb01
+ * a multiple of 16, else P1X_EUNSUPPORTED).
  *   w          M rows of GGUF blocks, row stride nb01 bytes (>= K/blk*blk_bytes, even; a multiple of 4 for
  *              q4_K); w 4-byte aligned.
  *   x          f32 [ncols][K]; K a multiple of the type's block size (32, or 256 for q4_K / q6_K).

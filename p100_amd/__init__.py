@@ -217,7 +217,7 @@ def mul_mat_vec(wtype, w, M, K, x, act="q8_1", nb01=None, group_sums=False, out=
     """dst[ncols, M] = src1[ncols, K] @ deq(src0[M, K])^T.
 
     w: uint8 device tensor holding M rows of GGUF blocks with row stride nb01 bytes; x: float32 [ncols, K]
-    (ncols 1..8; 1..16 for q4_0 / q8_0 / q4_K with act="q8_1") or a prepared Q81 / H16 activation. Returns y (and the int32 group sums [ncols, M, K/G] when
+    (ncols 1..8; 1..16 with act="q8_1") or a prepared Q81 / H16 activation. Returns y (and the int32 group sums [ncols, M, K/G] when
     group_sums=True, Q8_1 only).
     """
     import torch

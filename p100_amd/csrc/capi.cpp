@@ -90,7 +90,7 @@ int check_matvec(int wtype, const void* w, int64_t nb01, int64_t M, int64_t K, i
     if (M <= 0 || K <= 0 || M > INT32_MAX || K > INT32_MAX) return fail(P1X_EINVAL, "M and K must be in 1..INT_MAX");
     if (K % block_elems(wtype)) return fail(P1X_EINVAL, "K must be a multiple of the block size");
     if (ncols < 1 || ncols > max_cols)
-        return fail(P1X_EINVAL, max_cols == 8 ? "ncols (ne11) must be 1..8 (up to 16 for q4_0 / q8_0 / q4_K with a Q8_1 activation)"
+        return fail(P1X_EINVAL, max_cols == 8 ? "ncols (ne11) must be 1..8 (up to 16 with a Q8_1 activation)"
                                               : "ncols (ne11) must be 1..16");
     if (nb01 < K / block_elems(wtype) * block_bytes(wtype)) return fail(P1X_EINVAL, "row stride nb01 shorter than a row");
     if (nb01 % 2) return fail(P1X_EINVAL, "row stride nb01 must be even (GGUF blocks are 2-byte aligned)");

@@ -70,7 +70,7 @@ hipError_t launch_mmvq_swiglu(int type, const void* w, int64_t nb01, int F, int 
 bool mmvq_rope_kv_supported(int type, int M, int K, int d);
 hipError_t launch_mmvq_rope_kv(int type, const void* w, int64_t nb01, int M, int K, const int8_t* xq, const float* xds,
                                const RopeKv& rk, hipStream_t stream);
-// Several activation columns on int8 matrix cores (mmq.hip): q4_0 / q8_0 / q4_K weights, 1..kMmqMaxCols columns of a
+// Several activation columns on int8 matrix cores (mmq.hip): q4_0 / q8_0 / q4_K / q6_K weights, 1..kMmqMaxCols columns of a
 // prepared Q8_1 activation.
 constexpr int kMmqMaxCols = 16;
 bool mmq_supported(int type, int B);

@@ -4,10 +4,10 @@
 // v_mfma_i32_16x16x32_i8, so one instruction yields the exact int32 block sums of 16 weight rows x 16 columns
 // (the reference's per-block integer dot products, bit for bit); each block's sums are then scaled in FP32 with
 // the same per-block formula as the dot4 path (src/reference/qmv_model.cpp q81 path: q4_0 d*(dot*d8 - 8*s8),
-// q8_0 d*d8*dot, q4_K d8*(d*sc*dot - dmin*mn*isum) per 32-element sub-block). Where the dot4 path re-reads every
-// activation column for every weight row, here one wave
-// serves 16 rows per activation read, which is what makes many columns cheap (used from 9 columns, and from 5-7
-// on rows longer than 8192).
+// q8_0 d*d8*dot, q4_K d8*(d*sc*dot - dmin*mn*isum) per 32-element sub-block; q6_K two MFMAs per block, one per
+// 16-element half and its scale). Where the dot4 path re-reads every activation column for every weight row, here
+// one wave serves 16 rows per activation read, which is what makes many columns cheap (from 9 columns always, and
+// below that where measured faster: mmq_preferred).
 //
 // Lane layout of v_mfma_i32_16x16x32_i8 (checked on the device): A (16 x 32) lane l holds row l % 16, elements
 // 8 (l / 16) .. + 7; B (32 x 16) lane l holds column l % 16, the same elements; D (16 x 16) lane l holds rows
@@ -15,9 +15,9 @@
 // activation column (one scale load) and need the weight scales of four rows (read from the staged rows in LDS).
 //
 // Work-group: 16 weight rows, 8 waves (up to 8192 rows) or 4, each over a contiguous share of the K blocks, 8
-// blocks per step (one super-block for q4_K) staged through the wave's own LDS area with the next step's loads in
-// flight; the partial
-// 16 x 16 tiles are added in LDS in a fixed order (deterministic, no workspace). Grid: ceil(M / 16).
+// blocks per step (one super-block for q4_K / q6_K) staged through the wave's own LDS area with the next step's
+// loads in flight; the partial 16 x 16 tiles are added in LDS in a fixed order (deterministic, no workspace).
+// Grid: ceil(M / 16).
 #include <type_traits>
 
 #include "common.h"
@@ -39,6 +39,7 @@ struct MfmaW;
 template <>
 struct MfmaW<Q4_0> {
     static constexpr int kBytes = 18;
+    static constexpr int kSuper = 0;  // super-block bytes (a step is one super-block) or 0
     static constexpr bool kMins = false;
     static __device__ __forceinline__ float acc(float dw, float, int dot, float4 xs, float a) {
         return fmaf(dw, fmaf(float(dot), xs.x, -8.0f * xs.y), a);
@@ -49,6 +50,7 @@ struct MfmaW<Q4_0> {
 template <>
 struct MfmaW<Q8_0> {
     static constexpr int kBytes = 34;
+    static constexpr int kSuper = 0;
     static constexpr bool kMins = false;
     static __device__ __forceinline__ float acc(float dw, float, int dot, float4 xs, float a) {
         return fmaf(dw * xs.x, float(dot), a);
@@ -62,9 +64,25 @@ struct MfmaW<Q8_0> {
 template <>
 struct MfmaW<Q4_K> {
     static constexpr int kBytes = 18;
+    static constexpr int kSuper = 144;
     static constexpr bool kMins = true;
     static __device__ __forceinline__ float acc(float dw, float dm, int dot, float4 xs, float a) {
         return fmaf(xs.x, fmaf(dw, float(dot), -dm * xs.z), a);
+    }
+};
+
+// q6_K: 210-byte super-block {ql[128], qh[64], int8 scales[16], fp16 d}; 32-element block j = 4n + m takes the low
+// (m < 2) or high nibbles of ql[64n + 32 (m % 2) ..] and bits 2m, 2m + 1 of qh[32n ..], minus 32, and has one int8
+// scale per 16-element half (scales[2j], scales[2j + 1]). The halves are summed by separate MFMAs (the other half's
+// lanes zeroed), dw = d * sc_lo and dm = d * sc_hi: acc + d8 * (dw * dot_lo + dm * dot_hi), the reference's
+// per-call d * sum(d8 * dot * sc) (vec_dot_q6_K_q8_1, two 4-element halves per call) regrouped per block.
+template <>
+struct MfmaW<Q6_K> {
+    static constexpr int kBytes = 0;  // not a whole number per 32-element block: addressed per super-block
+    static constexpr int kSuper = 210;
+    static constexpr bool kMins = true;
+    static __device__ __forceinline__ float acc2(float dw, float dm, int lo, int hi, float4 xs, float a) {
+        return fmaf(xs.x, fmaf(dw, float(lo), dm * float(hi)), a);
     }
 };
 
@@ -75,7 +93,7 @@ struct MfmaW<Q4_K> {
 #define P1X_MMQ_STEP_Q4_0 8  // K blocks per step (staged through LDS) for q4_0 (16: slower); q8_0 takes 8
 #endif
 template <int TYPE>
-constexpr int step_blocks() { return TYPE == Q4_0 ? P1X_MMQ_STEP_Q4_0 : 8; }  // q4_K: one super-block
+constexpr int step_blocks() { return TYPE == Q4_0 ? P1X_MMQ_STEP_Q4_0 : 8; }  // q4_K / q6_K: one super-block
 #ifndef P1X_MMQ_PF
 #define P1X_MMQ_PF 1  // steps whose loads are in flight per wave (1 or 2; 2 measured slower)
 #endif
@@ -127,10 +145,12 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
     constexpr int U = step_blocks<TYPE>();
     static_assert(U == 8 || U == 16, "activation staging covers 8 or 16 blocks per step");
     constexpr int BB = W::kBytes;
-    constexpr int NWL = (U * BB + 4 + 63) / 64;  // 16-byte loads per lane (4 lanes per row)
-    static_assert(!ALN || (U * BB) % 16 == 0, "aligned steps are whole 16-byte chunks");
-    static_assert(TYPE != Q4_K || (ALN && U == 8), "q4_K: aligned rows, one super-block per step");
-    constexpr int NCH = ALN ? U * BB / 16 : 4 * NWL;      // 16-byte chunks staged per row and step
+    constexpr int SB = W::kSuper ? W::kSuper : U * BB;  // bytes of one step of a row
+    constexpr int NWL = (SB + 4 + 63) / 64;             // 16-byte loads per lane (4 lanes per row)
+    static_assert(!ALN || SB % 16 == 0, "aligned steps are whole 16-byte chunks");
+    static_assert(!W::kSuper || U == 8, "one super-block per step");
+    static_assert(TYPE != Q4_K || ALN, "q4_K: aligned rows");
+    constexpr int NCH = ALN ? SB / 16 : 4 * NWL;          // 16-byte chunks staged per row and step
     constexpr int NLD = ALN ? (16 * NCH + 63) / 64 : NWL;  // weight loads per lane
     // Staged dwords per row. Padding spreads the 16 rows over LDS banks: aligned rows take a stride of 4 x an odd
     // count (16 distinct banks for the A-operand reads of one dword offset, whole 16-byte chunks kept aligned).
@@ -143,9 +163,12 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
     const int g = lane >> 4, i16 = lane & 15;
     const int m0 = blockIdx.x * 16;
     const int nblk = K / 32;
-    const int per = ALN ? (nblk + NW * U - 1) / (NW * U) * U : (nblk + NW - 1) / NW;
+    // Wave shares in whole steps where a step is a run of whole chunks or a super-block.
+    const int per = ALN || W::kSuper ? (nblk + NW * U - 1) / (NW * U) * U : (nblk + NW - 1) / NW;
     const int b0 = min(nblk, wave * per), b1 = min(nblk, b0 + per);
     MmqStage<ROWDW, U, BC, W::kMins>& st = stage[wave];
+    // Byte offset in a row of the step starting at block bs (a multiple of 8 for super-blocks).
+    auto step_off = [](int bs) { return W::kSuper ? uint32_t(bs / 8) * uint32_t(SB) : uint32_t(bs) * uint32_t(BB); };
 
     // Global side of the staging: lane (row lane/4, quarter lane%4) reads NWL x 16 bytes of its row's dword-aligned
     // span.
@@ -160,7 +183,7 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
     // MFMA side: the lane's A-operand row (i16) and the rows 4g..4g+3 whose scales it applies; byte 0 of each
     // row's staged span is the dword holding the row's first byte of the step.
     auto row_shift = [&](int row, int bs) {
-        return ALN ? 0 : int((size_t(min(m0 + row, M - 1)) * nb01 + size_t(bs) * BB) & 3);
+        return ALN ? 0 : int((size_t(min(m0 + row, M - 1)) * nb01 + step_off(bs)) & 3);
     };
     // Aligned staging: chunk ci = k * 64 + lane of the step is chunk ci % NCH of row ci / NCH.
     uint32_t arow_off[NLD];
@@ -181,9 +204,9 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
         if constexpr (ALN) {
 #pragma unroll
             for (int k = 0; k < NLD; ++k)
-                rw[S][k] = ld16(wr, k * 64 + lane < 16 * NCH && live ? arow_off[k] + uint32_t(bs) * BB : kOob);
+                rw[S][k] = ld16(wr, k * 64 + lane < 16 * NCH && live ? arow_off[k] + step_off(bs) : kOob);
         } else {
-            const uint32_t wb = live ? (srow_off + uint32_t(bs) * BB) & ~3u : kOob;
+            const uint32_t wb = live ? (srow_off + step_off(bs)) & ~3u : kOob;
 #pragma unroll
             for (int k = 0; k < NWL; ++k) rw[S][k] = ld16(wr, wb + (sq * NWL + k) * 16);
         }
@@ -242,6 +265,22 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
             const uint2 q2 = *reinterpret_cast<const uint2*>(&st.w[i16][4 + 8 * (u >> 1) + 2 * g]);
             const uint32_t shn = 4u * (u & 1);
             wa = long((q2.x >> shn) & 0x0F0F0F0Fu) | (long((q2.y >> shn) & 0x0F0F0F0Fu) << 32);
+        } else if constexpr (TYPE == Q6_K) {
+            // Block u = 4n + m: low 4 bits from ql[64n + 32 (m % 2) + 8g ..] (nibble m / 2), high 2 bits from
+            // qh[32n + 8g ..] >> 2m; codes 0..63 to signed c - 32 per byte (bit 5 flipped; bits 6-7 set where it
+            // was clear, so no borrow crosses a byte).
+            const int n = u >> 2, m = u & 3;
+            uint32_t ql[2], qh[2];
+            bytes_at(i16, sh + 64 * n + 32 * (m & 1) + 8 * g, ql, 2);
+            bytes_at(i16, sh + 128 + 32 * n + 8 * g, qh, 2);
+            uint32_t v[2];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const uint32_t c = ((ql[k] >> (4 * (m >> 1))) & 0x0F0F0F0Fu) | (((qh[k] >> (2 * m)) & 0x03030303u) << 4);
+                const uint32_t z = ~c & 0x20202020u;
+                v[k] = (c ^ 0x20202020u) | (z << 2) | (z << 1);
+            }
+            wa = long(v[0]) | (long(v[1]) << 32);
         } else {
             uint32_t q2[2];
             bytes_at(i16, sh + u * BB + 2 + 8 * g, q2, 2);
@@ -250,21 +289,42 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
         const long xa = *reinterpret_cast<const long*>(&st.a[u][i16 % BC][2 * g]);
         const float4 xs = st.s[u][i16 % BC];
         const v4i zero = {0, 0, 0, 0};
-        const v4i dd = __builtin_amdgcn_mfma_i32_16x16x32_i8(wa, xa, zero, 0, 0, 0);
-        const float4 dw4 = *reinterpret_cast<const float4*>(&st.dw[u][4 * g]);
-        const float dw[4] = {dw4.x, dw4.y, dw4.z, dw4.w};
-        float dm[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if constexpr (W::kMins) {
+        if constexpr (TYPE == Q6_K) {  // elements 0..15 (lanes g < 2) and 16..31 with their own scales
+            const v4i dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(g < 2 ? wa : 0L, xa, zero, 0, 0, 0);
+            const v4i dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(g < 2 ? 0L : wa, xa, zero, 0, 0, 0);
+            const float4 dw4 = *reinterpret_cast<const float4*>(&st.dw[u][4 * g]);
             const float4 dm4 = *reinterpret_cast<const float4*>(&st.dm[u][4 * g]);
-            dm[0] = dm4.x, dm[1] = dm4.y, dm[2] = dm4.z, dm[3] = dm4.w;
-        }
+            const float dw[4] = {dw4.x, dw4.y, dw4.z, dw4.w}, dm[4] = {dm4.x, dm4.y, dm4.z, dm4.w};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float v = W::acc(dw[r], dm[r], dd[r], xs, acc[r]);
-            acc[r] = ok ? v : acc[r];
-            if (SUMS) {
-                const int m = m0 + 4 * g + r;
-                if (ok && i16 < B && m < M) gs[(size_t(i16) * M + m) * nblk + bs + u] = dd[r];
+            for (int r = 0; r < 4; ++r) {
+                const float v = W::acc2(dw[r], dm[r], dl[r], dh[r], xs, acc[r]);
+                acc[r] = ok ? v : acc[r];
+                if (SUMS) {
+                    const int m = m0 + 4 * g + r;
+                    if (ok && i16 < B && m < M) {
+                        int32_t* dst = gs + (size_t(i16) * M + m) * (2 * nblk) + 2 * (bs + u);
+                        dst[0] = dl[r];
+                        dst[1] = dh[r];
+                    }
+                }
+            }
+        } else {
+            const v4i dd = __builtin_amdgcn_mfma_i32_16x16x32_i8(wa, xa, zero, 0, 0, 0);
+            const float4 dw4 = *reinterpret_cast<const float4*>(&st.dw[u][4 * g]);
+            const float dw[4] = {dw4.x, dw4.y, dw4.z, dw4.w};
+            float dm[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if constexpr (W::kMins) {
+                const float4 dm4 = *reinterpret_cast<const float4*>(&st.dm[u][4 * g]);
+                dm[0] = dm4.x, dm[1] = dm4.y, dm[2] = dm4.z, dm[3] = dm4.w;
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float v = W::acc(dw[r], dm[r], dd[r], xs, acc[r]);
+                acc[r] = ok ? v : acc[r];
+                if (SUMS) {
+                    const int m = m0 + 4 * g + r;
+                    if (ok && i16 < B && m < M) gs[(size_t(i16) * M + m) * nblk + bs + u] = dd[r];
+                }
             }
         }
     };
@@ -291,6 +351,12 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
                 q4k_scale_min(st.w[row][1], st.w[row][2], st.w[row][3], u, sc, mn);
                 st.dw[u][row] = half_bits_to_float(h) * float(sc);
                 st.dm[u][row] = half_bits_to_float(h >> 16) * float(mn);
+            } else if constexpr (TYPE == Q6_K) {
+                const int sh = row_shift(row, bs);
+                const float d = half_bits_to_float(u16_at(row, sh + 208));
+                const uint32_t sc = u16_at(row, sh + 192 + 2 * u);  // int8 scales of the two halves
+                st.dw[u][row] = d * float(int8_t(sc & 255));
+                st.dm[u][row] = d * float(int8_t(sc >> 8));
             } else {
                 st.dw[u][row] = half_bits_to_float(u16_at(row, row_shift(row, bs) + u * BB));
             }
@@ -363,7 +429,7 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
 #endif
 
 bool mmq_supported(int type, int B) {
-    return (type == Q4_0 || type == Q8_0 || type == Q4_K) && B >= 1 && B <= kMmqMaxCols;
+    return (type == Q4_0 || type == Q8_0 || type == Q4_K || type == Q6_K) && B >= 1 && B <= kMmqMaxCols;
 }
 // The staging loads address the weight matrix through one 32-bit buffer range; q4_K stages whole 16-byte chunks
 // of its rows (a row stride of 16-byte multiples, as every unpadded q4_K row is).
@@ -394,9 +460,23 @@ bool mmq_fits(int type, int M, int64_t nb01, int K, int B) {
 #ifndef P1X_MMQ_MIN_COLS_Q4_K_FEW_ROWS
 #define P1X_MMQ_MIN_COLS_Q4_K_FEW_ROWS 8  // q4_K, fewer than 4096 rows
 #endif
+// q6_K (dot4 against the matrix cores, 1 / 2 / 4 / 5 / 8 columns): 4096x14336 15.1 / 21.1 / 33.1 / 39.1 / 53.9
+// against 20.3 / 18.7 / 20.2 / 19.0 / 19.6 us, 128256x4096 103.9 / 135.4 / 155.6 / - / 441.8 against 123.4 /
+// 123.6 / 126.7 / - / 133.2, 14336x4096 14.2 / 17.3 / 20.0 / 23.6 / 31.9 against 21.0 / 21.5 / 21.2 / 21.8 / 22.2,
+// 4096x4096 6.3 / 7.1 / 8.4 / 9.4 / 12.8 against 8.2 / 8.3 / 8.3 / 8.4 / 8.5, 1024x4096 3.8 / 4.2 / 4.9 / 5.3 /
+// 6.3 against 6.9 / 6.9 / 7.1 / 7.2 / 7.3 (the crossover between 14336 and 128256 rows at 2-4 columns is not
+// measured more finely).
+#ifndef P1X_MMQ_MIN_COLS_Q6_K_LONG
+#define P1X_MMQ_MIN_COLS_Q6_K_LONG 2  // q6_K rows longer than 8192, or at least 65536 rows (of at least 4096)
+#endif
+#ifndef P1X_MMQ_MIN_COLS_Q6_K
+#define P1X_MMQ_MIN_COLS_Q6_K 5  // q6_K rows of at most 8192 on 4096..65535 rows
+#endif
 bool mmq_preferred(int type, int B, int M, int K) {
     if (!mmq_supported(type, B)) return false;
     if (B >= P1X_MMQ_MIN_COLS) return true;
+    if (type == Q6_K)
+        return M >= 4096 && B >= (K > 8192 || M >= 65536 ? P1X_MMQ_MIN_COLS_Q6_K_LONG : P1X_MMQ_MIN_COLS_Q6_K);
     if (type == Q4_K)
         return M >= 4096 ? B >= (K > 8192 ? P1X_MMQ_MIN_COLS_Q4_K_LONG : P1X_MMQ_MIN_COLS_Q4_K)
                          : B >= P1X_MMQ_MIN_COLS_Q4_K_FEW_ROWS;
@@ -440,6 +520,9 @@ hipError_t launch_mmq(int type, int B, const void* w, int64_t nb01, int M, int K
         // Rows of whole 16-byte chunks from a 4-byte aligned base: the 16-byte buffer loads need dword alignment.
         if (gs) P1X_MMQ_L(Q4_K, true, true);
         else P1X_MMQ_L(Q4_K, false, true);
+    } else if (type == Q6_K) {  // 210-byte super-blocks: dword-aligned spans with a 0 / 2 byte shift
+        if (gs) P1X_MMQ_L(Q6_K, true, false);
+        else P1X_MMQ_L(Q6_K, false, false);
     } else {
         return hipErrorInvalidValue;
     }

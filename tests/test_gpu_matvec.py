@@ -178,7 +178,7 @@ def test_many_columns_parity(orc, gpu, tname):
             assert (y3.view(np.uint32) == y2.view(np.uint32)).all()
 
 
-def _q4_k_case(orc, t, w, x, rows, k, nb01=None, offset=0):
+def _kquant_case(orc, t, w, x, rows, k, nb01=None, offset=0):
     """q4_K through the fp32 op (with and without group sums) and a prepared activation, the weights at nb01 bytes
     per row from byte `offset` of a device buffer: sums bit-exact, FP32 within the bars, the fp32 op's two calls alike
     bit for bit, and the prepared activation's too on the matrix cores (9..16 columns; at 1..8 the fp32 op may take
@@ -215,10 +215,10 @@ def test_q4_K_many_columns(orc, gpu):
     for k, rows in ((256, 17), (512, 16), (256, 33), (4096, 17), (14336, 33), (4096, 4096), (256, 8200)):
         for ncols in ((9, 12, 16) if rows < 4096 else (16,)):
             w, x = make_case(orc, t, k, rows, ncols, seed=3100 + k + rows + ncols)
-            _q4_k_case(orc, t, w, x, rows, k)
+            _kquant_case(orc, t, w, x, rows, k)
     w, x = make_case(orc, t, 512, 19, 12, seed=3201)
-    _q4_k_case(orc, t, w, x, 19, 512, offset=4)
-    _q4_k_case(orc, t, w, x, 19, 512, nb01=w.shape[1] + 16, offset=8)
+    _kquant_case(orc, t, w, x, 19, 512, offset=4)
+    _kquant_case(orc, t, w, x, 19, 512, nb01=w.shape[1] + 16, offset=8)
 
 
 def test_q4_K_few_columns_matrix_cores(orc, gpu):
@@ -229,7 +229,33 @@ def test_q4_K_few_columns_matrix_cores(orc, gpu):
     for k, rows, ncols in ((8448, 4100, 2), (8448, 4100, 5), (256, 4104, 3), (256, 4104, 8), (256, 8200, 3),
                            (1024, 40, 8)):
         w, x = make_case(orc, t, k, rows, ncols, seed=3400 + k + rows + ncols)
-        _q4_k_case(orc, t, w, x, rows, k)
+        _kquant_case(orc, t, w, x, rows, k)
+
+
+def test_q6_K_many_columns(orc, gpu):
+    """q6_K at 9..16 columns on the int8 matrix cores: one 210-byte super-block per step staged from the dword
+    holding its first byte (rows of an odd super-block count alternate a 0 / 2 byte shift), the 6-bit codes
+    rebuilt from ql nibbles and qh bit pairs as signed bytes, each 32-element block's two 16-element halves summed
+    by their own MFMA with their own int8 scale. Group sums (16 elements) bit-exact, FP32 within the bars; one and
+    two super-blocks per row (idle waves), partial 16-row tiles, the full-size shapes, past 8192 rows."""
+    t = orc.TYPES["q6_K"]
+    for k, rows in ((256, 17), (512, 16), (768, 33), (4096, 17), (14336, 33), (4096, 4096), (256, 8200)):
+        for ncols in ((9, 12, 16) if rows < 4096 else (16,)):
+            w, x = make_case(orc, t, k, rows, ncols, seed=3500 + k + rows + ncols)
+            _kquant_case(orc, t, w, x, rows, k)
+    w, x = make_case(orc, t, 512, 19, 10, seed=3601)
+    _kquant_case(orc, t, w, x, 19, 512, offset=4)
+    _kquant_case(orc, t, w, x, 19, 512, nb01=w.shape[1] + 6, offset=4)
+
+
+def test_q6_K_few_columns_matrix_cores(orc, gpu):
+    """q6_K at 2..8 columns where the matrix-core form takes the shape (from 2 columns on rows longer than 8192,
+    from 5 on rows of at most 8192 on at least 4096 rows): 8 staged activation columns, 8 waves per work-group up
+    to 8192 rows and 4 beyond, 2-byte shifted rows, partial last row tiles; sums bit-exact, FP32 within the bars."""
+    t = orc.TYPES["q6_K"]
+    for k, rows, ncols in ((8448, 4100, 2), (8448, 4100, 7), (256, 4105, 5), (256, 8200, 8), (768, 4097, 6)):
+        w, x = make_case(orc, t, k, rows, ncols, seed=3700 + k + rows + ncols)
+        _kquant_case(orc, t, w, x, rows, k)
 
 
 def test_q4_K_many_columns_unaligned_stride(orc, gpu):
@@ -244,7 +270,7 @@ def test_q4_K_many_columns_unaligned_stride(orc, gpu):
     pad[:, :rb] = w
     with pytest.raises(P.P1XError, match="16-byte"):
         P.mul_mat_vec(t, to_dev(pad), 17, 512, to_dev(x), nb01=rb + 4)
-    _q4_k_case(orc, t, w, x[:8], 17, 512, nb01=rb + 4)
+    _kquant_case(orc, t, w, x[:8], 17, 512, nb01=rb + 4)
 
 
 @pytest.mark.parametrize("tname", ["q4_0", "q8_0"])
@@ -411,10 +437,10 @@ def test_invalid_arguments(gpu):
         P.mul_mat_vec("q4_K", w, 1, 32, x)
     with pytest.raises(ValueError, match="ncols"):
         P.mul_mat_vec("q4_0", w, 1, 32, torch.zeros((17, 32), device="cuda"))
-    with pytest.raises(ValueError, match="ncols"):  # 9..16 columns: q4_0 / q8_0 / q4_K with a Q8_1 activation only
+    with pytest.raises(ValueError, match="ncols"):  # 9..16 columns: with a Q8_1 activation only
         P.mul_mat_vec("q4_0", w, 1, 32, torch.zeros((9, 32), device="cuda"), act="h16")
     with pytest.raises(ValueError, match="ncols"):
-        P.mul_mat_vec("q6_K", w, 1, 256, torch.zeros((9, 256), device="cuda"))
+        P.mul_mat_vec("q6_K", w, 1, 256, torch.zeros((17, 256), device="cuda"))
     with pytest.raises(ValueError, match="row stride"):
         P.mul_mat_vec("q4_0", w, 1, 32, x, nb01=16)
     with pytest.raises(P.P1XError):
