@@ -535,7 +535,8 @@ KQUANT_SHAPES = [("q4_K", 14336, 4096), ("q4_K", 4096, 14336), ("q6_K", 128256, 
 
 def measure_kquant(torch, P, lib, synth, timer, gen, only=None):
     """The K-quant configuration at ne11 = 1: Q4_K FFN matrices and the Q6_K output projection, as the whole op
-    from an f32 activation (Q8_1 quantize + mat-vec) and as the mat-vec kernel on a prepared activation."""
+    from an f32 activation (Q8_1 quantize + mat-vec) and as the mat-vec kernel on a prepared activation; and the
+    kernel at 8 and 16 columns."""
     out = {}
     for tname, M, K in KQUANT_SHAPES:
         key = f"{tname}:{M}x{K}"
@@ -547,6 +548,11 @@ def measure_kquant(torch, P, lib, synth, timer, gen, only=None):
         out[f"{tname} {M}x{K} n=1"] = {"kernel": kern, "op": op}
         log(f"[bench] {tname} {M}x{K}: kernel {kern['us']} us ({kern['gbs']} GB/s, frac {kern['frac']}), "
             f"op {op['us']} us")
+        # The same matrices at 8 and 16 columns (int8 matrix cores), kernel on a prepared activation.
+        for n in (8, 16):
+            kn = measure_matvec(torch, P, lib, synth, timer, gen, t, M, K, n, prepared=True)
+            out[f"{tname} {M}x{K} n={n}"] = {"kernel": kn}
+            log(f"[bench] {tname} {M}x{K} n={n}: kernel {kn['us']} us ({kn['gbs']} GB/s)")
     return out
 
 
