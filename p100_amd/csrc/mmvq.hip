@@ -19,6 +19,8 @@
 // activation can also be the RMSNorm of the residual stream, normalized and quantized by every work-group
 // (SrcNorm), and its store step can add into a residual, apply RoPE and append to the KV cache, or write SwiGLU.
 // 2..8 columns of q4_0 / q8_0 take k_mmvr_cols where its plan applies (mmvr_cols_plan).
+#include <type_traits>
+
 #include "common.h"
 #include "launch.h"
 
@@ -138,6 +140,8 @@ __device__ __forceinline__ int dot8(const uint32_t* w, int4 x0, int4 x1) {
 // nibbles (qmv_model.cpp:151-160); one call per block here: fma(d, fma(float(dot), d8, -8 s8), acc).
 struct UnitQ4_0 {
     static constexpr int kElems = 32, kGroups = 1, kActBlocks = 1;
+    static __device__ __forceinline__ int act_index(int u, int ab) { return u + ab; }
+    static __device__ __forceinline__ int group_index(int u, int k) { return u + k; }
     uint32_t w[5], sh;
     __device__ __forceinline__ void load(const uint8_t* row, int u) {
         const uintptr_t a = reinterpret_cast<uintptr_t>(row + size_t(u) * 18);
@@ -166,6 +170,8 @@ struct UnitQ4_0 {
 // q8_0: 34-byte block {fp16 d, int8 qs[32]}; reference: fma(d * d8, float(dot), acc) (qmv_model.cpp:161).
 struct UnitQ8_0 {
     static constexpr int kElems = 32, kGroups = 1, kActBlocks = 1;
+    static __device__ __forceinline__ int act_index(int u, int ab) { return u + ab; }
+    static __device__ __forceinline__ int group_index(int u, int k) { return u + k; }
     uint32_t w[9], sh;
     __device__ __forceinline__ void load(const uint8_t* row, int u) {
         const uintptr_t a = reinterpret_cast<uintptr_t>(row + size_t(u) * 34);
@@ -193,6 +199,8 @@ struct UnitQ8_0 {
 // (q4k_scale_min). Value = d*sc*q - dmin*mn; Q8_1 terms d8*dot*sc and d8*isum*mn (qmv_model.cpp:166-178).
 struct UnitQ4_K {
     static constexpr int kElems = 64, kGroups = 2, kActBlocks = 2;
+    static __device__ __forceinline__ int act_index(int u, int ab) { return 2 * u + ab; }
+    static __device__ __forceinline__ int group_index(int u, int k) { return 2 * u + k; }
     uint32_t hdr[4], q[8];
     int g;
     __device__ __forceinline__ void load(const uint8_t* row, int u) {
@@ -227,8 +235,10 @@ struct UnitQ4_K {
 // Element i of s: low 4 bits from ql[(s/4)*64 + (s%2)*32 + i] (low nibble for s%4 < 2, else high), high 2 bits
 // from qh[(s/4)*32 + i] >> 2*(s%4); q6 = value - 32; scale per 16 = scales[2s + i/16] (ggml dequantize_row_q6_K).
 // Reference arithmetic (vec_dot_q6_K_q8_1): d * sum(d8 * dot16 * sc) with exact int32 dot16 per 16 elements.
-struct UnitQ6_K {
+struct UnitQ6_K32 {
     static constexpr int kElems = 32, kGroups = 2, kActBlocks = 1;
+    static __device__ __forceinline__ int act_index(int u, int ab) { return u + ab; }
+    static __device__ __forceinline__ int group_index(int u, int k) { return 2 * u + k; }
     uint32_t ql[8], qh[8], sw, dw;
     int s;
     __device__ __forceinline__ void load(const uint8_t* row, int u) {
@@ -268,16 +278,81 @@ struct UnitQ6_K {
     }
 };
 
+// q6_K by sub-block pairs: unit u holds sub-blocks s0 = 4 (q / 2) + q % 2 and s0 + 2 (q = u % 4) of super-block
+// u / 4, which share ql[64 (s0 / 4) + 32 (s0 % 2) ..] (low / high nibbles) and qh[32 (s0 / 4) ..] (bits 2 (s0 % 4)
+// and 2 (s0 % 4) + 4), so one load and one re-slice of the 2-byte-aligned fields serve 64 elements (the 32-element
+// unit above loads and re-slices both fields for each sub-block). Its activation blocks and 16-element group sums
+// are those of the two sub-blocks (not adjacent in K). The arithmetic per sub-block is UnitQ6_K32's.
+struct UnitQ6_K {
+    static constexpr int kElems = 64, kGroups = 4, kActBlocks = 2;
+    static __device__ __forceinline__ int act_index(int u, int ab) {
+        const int q = u & 3;
+        return 8 * (u >> 2) + 4 * (q >> 1) + (q & 1) + 2 * ab;
+    }
+    static __device__ __forceinline__ int group_index(int u, int k) { return 2 * act_index(u, k >> 1) + (k & 1); }
+    uint32_t ql[8], qh[8], sc[2], dw;
+    int hsh;
+    __device__ __forceinline__ void load(const uint8_t* row, int u) {
+        const int q = u & 3, s0 = 4 * (q >> 1) + (q & 1);
+        hsh = 2 * (s0 & 3);
+        const uint8_t* p = row + size_t(u >> 2) * 210;
+        load_field<8>(p + (s0 >> 2) * 64 + (s0 & 1) * 32, ql);
+        load_field<8>(p + 128 + (s0 >> 2) * 32, qh);
+        sc[0] = load_u16(p + 192 + 2 * s0);  // scales[2 s0], [2 s0 + 1]
+        sc[1] = load_u16(p + 196 + 2 * s0);  // scales[2 s0 + 4], [2 s0 + 5]: sub-block s0 + 2
+        dw = load_u16(p + 208);
+    }
+    // One sub-block: codes v (0..63) into the signed dot4 unchanged, -32 per code as -32 * sum(x) per half.
+    static __device__ __forceinline__ float sub(const uint32_t* v, const ActBlock& x, uint32_t s2, float d, float a,
+                                                int32_t* g) {
+        constexpr int kOnes = 0x01010101;
+        int slo = dot4(kOnes, x.lo.x, 0);
+        slo = dot4(kOnes, x.lo.y, slo);
+        slo = dot4(kOnes, x.lo.z, slo);
+        slo = dot4(kOnes, x.lo.w, slo);
+        const int shi = int(x.ds.z) - slo;  // isum is exact in the float
+        int g0 = dot4(int(v[0]), x.lo.x, -32 * slo);
+        g0 = dot4(int(v[1]), x.lo.y, g0);
+        g0 = dot4(int(v[2]), x.lo.z, g0);
+        g0 = dot4(int(v[3]), x.lo.w, g0);
+        int g1 = dot4(int(v[4]), x.hi.x, -32 * shi);
+        g1 = dot4(int(v[5]), x.hi.y, g1);
+        g1 = dot4(int(v[6]), x.hi.z, g1);
+        g1 = dot4(int(v[7]), x.hi.w, g1);
+        g[0] = g0;
+        g[1] = g1;
+        const int sc0 = int(int8_t(s2 & 255)), sc1 = int(int8_t((s2 >> 8) & 255));
+        return fmaf(d * x.ds.x, float(g0 * sc0 + g1 * sc1), a);
+    }
+    __device__ __forceinline__ float acc(const ActBlock* x, float a, int32_t* g) const {
+        uint32_t va[8], vb[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            va[j] = (ql[j] & kLo) | (((qh[j] >> hsh) & 0x03030303u) << 4);
+            vb[j] = ((ql[j] >> 4) & kLo) | (((qh[j] >> (hsh + 4)) & 0x03030303u) << 4);
+        }
+        const float d = half_bits_to_float(dw);
+        a = sub(va, x[0], sc[0], d, a, g);
+        return sub(vb, x[1], sc[1], d, a, g + 2);
+    }
+};
+#ifndef P1X_MMVQ_Q6K_PAIR
+#define P1X_MMVQ_Q6K_PAIR 1  // one q6_K column on rows of 4096-multiples: units of two sub-blocks sharing their fields
+#endif
+// Kernel-template tag of q6_K with UnitQ6_K (not a weight type of the interface).
+constexpr int kQ6_KPair = 0x100 | Q6_K;
+
 template <int TYPE> struct UnitOf;
 template <> struct UnitOf<Q4_0> { using T = UnitQ4_0; };
 template <> struct UnitOf<Q8_0> { using T = UnitQ8_0; };
 template <> struct UnitOf<Q4_K> { using T = UnitQ4_K; };
-template <> struct UnitOf<Q6_K> { using T = UnitQ6_K; };
+template <> struct UnitOf<Q6_K> { using T = UnitQ6_K32; };
+template <> struct UnitOf<kQ6_KPair> { using T = UnitQ6_K; };
 
 // Units per lane per pass: register budget for B activation columns (more columns, fewer units).
 template <int TYPE, int B>
 constexpr int units_per_lane() {
-    if (TYPE == Q4_K || TYPE == Q6_K) return 1;
+    if (TYPE == Q4_K || TYPE == Q6_K || TYPE == kQ6_KPair) return 1;
     return B <= 2 ? P1X_MMVQ_UB : 1;
 }
 
@@ -355,7 +430,7 @@ __device__ __forceinline__ void mmvq_rows(const Act act, Prep prep, const uint8_
 #pragma unroll
             for (int c = 0; c < B; ++c)
 #pragma unroll
-                for (int ab = 0; ab < U::kActBlocks; ++ab) x[i][c][ab] = act.get(c, unit_of(kc, i) * U::kActBlocks + ab);
+                for (int ab = 0; ab < U::kActBlocks; ++ab) x[i][c][ab] = act.get(c, U::act_index(unit_of(kc, i), ab));
 #pragma unroll
         for (int r = 0; r < RW; ++r) {
             const bool rok = r0 + r < M;
@@ -369,9 +444,9 @@ __device__ __forceinline__ void mmvq_rows(const Act act, Prep prep, const uint8_
                     const float v = wu[r][i].acc(x[i][c], acc[r][c], g);
                     acc[r][c] = uok ? v : acc[r][c];
                     if (SUMS && uok && rok) {
-                        int32_t* dst = gs + (size_t(c) * M + r0 + r) * glen + size_t(u) * U::kGroups;
+                        int32_t* dst = gs + (size_t(c) * M + r0 + r) * glen;
 #pragma unroll
-                        for (int k = 0; k < U::kGroups; ++k) dst[k] = g[k];
+                        for (int k = 0; k < U::kGroups; ++k) dst[U::group_index(u, k)] = g[k];
                     }
                 }
             }
@@ -1073,7 +1148,13 @@ hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int 
         case Q4_0: return launch_type<Q4_0>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
         case Q8_0: return launch_type<Q8_0>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
         case Q4_K: return launch_type<Q4_K>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
-        case Q6_K: return launch_type<Q6_K>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
+        case Q6_K:
+            // One column on rows of whole 64-unit passes: the paired unit (128256x4096 105.5 -> 95.1 us, 14336x4096
+            // 14.2 -> 13.6); on 14336-long rows (3.5 passes) and at 2+ columns (twice the activation registers) the
+            // one-sub-block unit is faster (4096x14336 15.8 against 18.9 us).
+            if (P1X_MMVQ_Q6K_PAIR && B == 1 && K % 4096 == 0)
+                return launch_b<kQ6_KPair, 1>(wb, nb01, M, K, rw, xq, d4, x, y, gs, stream, Slices{});
+            return launch_type<Q6_K>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
     }
     return hipErrorInvalidValue;
 }
