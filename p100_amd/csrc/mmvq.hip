@@ -57,6 +57,9 @@
 #ifndef P1X_MMVR_ENABLE
 #define P1X_MMVR_ENABLE 1  // one prepared q4_0 / q8_0 column: register-resident activation kernel (k_mmvr)
 #endif
+#ifndef P1X_MMVR_Q4_K
+#define P1X_MMVR_Q4_K 1  // one prepared q4_K column on k_mmvr too, on at most 4096 x 4096
+#endif
 #ifndef P1X_MMVR_FUSED
 #define P1X_MMVR_FUSED 1  // one f32 q4_0 / q8_0 column in one launch: k_mmvr quantizing x per work-group
 #endif
@@ -750,7 +753,7 @@ __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int
     static_assert(!EPI::kPairs || R % 2 == 0, "row pairs stay inside one row-group");
 
     using U = typename UnitOf<TYPE>::T;
-    static_assert(U::kActBlocks == 1 && U::kGroups == 1, "one Q8_1 block and one int32 sum per unit");
+    constexpr int NA = U::kActBlocks;  // Q8_1 blocks per unit (2 for a q4_K sub-block pair)
     constexpr int T = 64 * NWK, G = 4 / NWK;
     __shared__ float red[4][R];
     const int tid = threadIdx.x, g = tid / T, t = tid - g * T;
@@ -758,7 +761,7 @@ __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int
     const int row0 = (blockIdx.x * G + g) * R;
     const int epi_in = epi.start();
     constexpr int NV = SRC::kNV;
-    ActBlock x[UPT];
+    ActBlock x[UPT][NA];
     int uc[UPT];
     bool uok[UPT];
     NormIn<NV> nin;
@@ -768,7 +771,9 @@ __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int
         const int u = t + T * j;
         uok[j] = u < units;
         uc[j] = uok[j] ? u : 0;
-        if constexpr (NV == 0) x[j] = ActGlobal{src.xq, src.xds, K}.get(0, uc[j]);
+        if constexpr (NV == 0)
+#pragma unroll
+            for (int ab = 0; ab < NA; ++ab) x[j][ab] = ActGlobal{src.xq, src.xds, K}.get(0, U::act_index(uc[j], ab));
     }
     U wv[R][UPT];
 #pragma unroll
@@ -781,9 +786,11 @@ __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int
     if constexpr (NV > 0) {  // the weight stream stays in flight across the barriers (they wait for LDS only)
         __shared__ NormLds<NV> nl;
         norm_q8_1_to_lds<SRC::kNorm>(nin, K, src.eps, nl);
-        const ActLds al{nl.lo, nl.hi, nl.ds, units};
+        const ActLds al{nl.lo, nl.hi, nl.ds, K / 32};
 #pragma unroll
-        for (int j = 0; j < UPT; ++j) x[j] = al.get(0, uc[j]);
+        for (int j = 0; j < UPT; ++j)
+#pragma unroll
+            for (int ab = 0; ab < NA; ++ab) x[j][ab] = al.get(0, U::act_index(uc[j], ab));
     }
     float acc[R];
 #pragma unroll
@@ -791,10 +798,13 @@ __global__ __launch_bounds__(256) void k_mmvr(const uint8_t* __restrict__ w, int
         float a = 0.0f;
 #pragma unroll
         for (int j = 0; j < UPT; ++j) {
-            int32_t gg[1];
-            const float v = wv[r][j].acc(&x[j], a, gg);
+            int32_t gg[U::kGroups];
+            const float v = wv[r][j].acc(x[j], a, gg);
             a = uok[j] ? v : a;
-            if (SUMS && uok[j] && row0 + r < M) gs[size_t(row0 + r) * units + t + T * j] = gg[0];
+            if (SUMS && uok[j] && row0 + r < M)
+#pragma unroll
+                for (int k = 0; k < U::kGroups; ++k)
+                    gs[size_t(row0 + r) * units * U::kGroups + U::group_index(t + T * j, k)] = gg[k];
         }
         acc[r] = wave_total(a);
     }
@@ -840,7 +850,7 @@ struct MmvrPlan {
     int nwk, upt, r;
 };
 bool mmvr_plan(int type, int M, int K, MmvrPlan& p) {
-    const int units = K / 32;
+    const int units = K / (type == Q4_K ? 64 : 32);  // q4_K: sub-block pairs
     if (units <= 64) {
         p = {1, 1, 2};
     } else if (units <= 128) {
@@ -1141,6 +1151,12 @@ hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int 
     if (B == 1 && !x && P1X_MMVR_ENABLE && (type == Q4_0 || type == Q8_0) && mmvr_plan(type, M, K, plan))
         return type == Q4_0 ? launch_mmvr<Q4_0>(plan, wb, nb01, M, K, SrcQ81{xq, d4}, EpiRows{y, nullptr}, gs, stream)
                             : launch_mmvr<Q8_0>(plan, wb, nb01, M, K, SrcQ81{xq, d4}, EpiRows{y, nullptr}, gs, stream);
+    // q4_K units are sub-block pairs with two Q8_1 blocks each, so every wave of k_mmvr reads 96 activation bytes
+    // per unit from L2: faster than the LDS-staged kernel on 4096x4096 (4.37 against 4.62 us) and 1024x4096
+    // (2.97 / 3.06), slower on 14336x4096 (9.73 / 8.99) and 4096x14336 (11.13 / 9.85).
+    if (B == 1 && !x && P1X_MMVR_ENABLE && P1X_MMVR_Q4_K && type == Q4_K && M <= 4096 && K <= 4096 &&
+        mmvr_plan(type, M, K, plan))
+        return launch_mmvr<Q4_K>(plan, wb, nb01, M, K, SrcQ81{xq, d4}, EpiRows{y, nullptr}, gs, stream);
     if (B == 1 && x && P1X_MMVR_FUSED && (type == Q4_0 || type == Q8_0) && mmvr_norm_plan(type, M, K, plan))
         return type == Q4_0 ? launch_mmvr_f32<Q4_0>(plan, wb, nb01, M, K, x, y, gs, stream)
                             : launch_mmvr_f32<Q8_0>(plan, wb, nb01, M, K, x, y, gs, stream);
