@@ -339,6 +339,21 @@ def test_mmvq_activation_ranges(orc, gpu, tname, scale):
 
 
 @pytest.mark.parametrize("tname", TYPES)
+@pytest.mark.parametrize("scale", [1e5, 1e-5])
+def test_matrix_core_activation_ranges(orc, gpu, tname, scale):
+    """The int8 matrix-core form (9 and 16 columns, every type) under the x1e5 / x1e-5 activation ranges: at 1e5
+    the Q8_1 block sums overflow fp16 (s = inf), which only the q4_0 formula reads; sums bit-exact, finiteness
+    as the oracle's, FP32 within the bars."""
+    import p100_amd as P
+
+    t = orc.TYPES[tname]
+    for ncols in (9, 16):
+        w, x = make_case(orc, t, 4096, 33, ncols, seed=1600 + ncols, scale=scale)
+        y, sums = P.mul_mat_vec(t, to_dev(w), 33, 4096, to_dev(x), act="q8_1", group_sums=True)
+        check_matvec(orc, t, w, x, y.cpu().numpy(), sums.cpu().numpy(), "q81")
+
+
+@pytest.mark.parametrize("tname", TYPES)
 def test_mmvh_parity(orc, gpu, tname):
     import p100_amd as P
 
