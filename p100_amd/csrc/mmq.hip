@@ -100,6 +100,9 @@ constexpr int step_blocks() { return TYPE == Q4_0 ? P1X_MMQ_STEP_Q4_0 : 8; }  //
 #ifndef P1X_MMQ_UNROLL
 #define P1X_MMQ_UNROLL 8  // blocks of a step unrolled together (more keeps too many operands live)
 #endif
+#ifndef P1X_MMQ_PHASED
+#define P1X_MMQ_PHASED 1  // a step's operand reads, MFMAs and epilogues as three phases (0: block by block)
+#endif
 #ifndef P1X_MMQ_CLAMP
 #define P1X_MMQ_CLAMP 1  // loads of steps past the wave's share read nothing (range-checked offset)
 #endif
@@ -248,23 +251,18 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
     };
 
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    // Block u of a step: the MFMA of row tile x column tile, then each lane's four (row, column) sums scaled into
-    // its accumulators. kTail: the last step of a share shorter than U blocks (the blocks past b1 are skipped).
-    auto block = [&](int bs, int u, int sh, auto tail_tag) {
-        constexpr bool kTail = decltype(tail_tag)::value;
-        const bool ok = !kTail || bs + u < b1;
-        // A operand: 8 weight elements 8g..8g+7 of block u of row i16.
-        long wa;
+    // A operand of block u: 8 weight elements 8g..8g+7 of row i16.
+    auto a_operand = [&](int u, int sh) -> long {
         if constexpr (TYPE == Q4_0) {
             uint32_t q2[2];
             bytes_at(i16, sh + u * BB + 2 + 8 * (g & 1), q2, 2);
             const uint32_t shn = (g & 2) ? 4u : 0u;
-            wa = long((q2[0] >> shn) & 0x0F0F0F0Fu) | (long((q2[1] >> shn) & 0x0F0F0F0Fu) << 32);
+            return long((q2[0] >> shn) & 0x0F0F0F0Fu) | (long((q2[1] >> shn) & 0x0F0F0F0Fu) << 32);
         } else if constexpr (TYPE == Q4_K) {
             // qs bytes 32 (u / 2) + 8g .. + 7 (super-block bytes 16 + ..., 8-byte aligned), nibble u % 2.
             const uint2 q2 = *reinterpret_cast<const uint2*>(&st.w[i16][4 + 8 * (u >> 1) + 2 * g]);
             const uint32_t shn = 4u * (u & 1);
-            wa = long((q2.x >> shn) & 0x0F0F0F0Fu) | (long((q2.y >> shn) & 0x0F0F0F0Fu) << 32);
+            return long((q2.x >> shn) & 0x0F0F0F0Fu) | (long((q2.y >> shn) & 0x0F0F0F0Fu) << 32);
         } else if constexpr (TYPE == Q6_K) {
             // Block u = 4n + m: low 4 bits from ql[64n + 32 (m % 2) + 8g ..] (nibble m / 2), high 2 bits from
             // qh[32n + 8g ..] >> 2m; codes 0..63 to signed c - 32 per byte (bit 5 flipped; bits 6-7 set where it
@@ -280,52 +278,79 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
                 const uint32_t z = ~c & 0x20202020u;
                 v[k] = (c ^ 0x20202020u) | (z << 2) | (z << 1);
             }
-            wa = long(v[0]) | (long(v[1]) << 32);
+            return long(v[0]) | (long(v[1]) << 32);
         } else {
             uint32_t q2[2];
             bytes_at(i16, sh + u * BB + 2 + 8 * g, q2, 2);
-            wa = long(q2[0]) | (long(q2[1]) << 32);
+            return long(q2[0]) | (long(q2[1]) << 32);
         }
-        const long xa = *reinterpret_cast<const long*>(&st.a[u][i16 % BC][2 * g]);
-        const float4 xs = st.s[u][i16 % BC];
-        const v4i zero = {0, 0, 0, 0};
-        if constexpr (TYPE == Q6_K) {  // elements 0..15 (lanes g < 2) and 16..31 with their own scales
-            const v4i dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(g < 2 ? wa : 0L, xa, zero, 0, 0, 0);
-            const v4i dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(g < 2 ? 0L : wa, xa, zero, 0, 0, 0);
-            const float4 dw4 = *reinterpret_cast<const float4*>(&st.dw[u][4 * g]);
-            const float4 dm4 = *reinterpret_cast<const float4*>(&st.dm[u][4 * g]);
-            const float dw[4] = {dw4.x, dw4.y, dw4.z, dw4.w}, dm[4] = {dm4.x, dm4.y, dm4.z, dm4.w};
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float v = W::acc2(dw[r], dm[r], dl[r], dh[r], xs, acc[r]);
-                acc[r] = ok ? v : acc[r];
-                if (SUMS) {
-                    const int m = m0 + 4 * g + r;
-                    if (ok && i16 < B && m < M) {
-                        int32_t* dst = gs + (size_t(i16) * M + m) * (2 * nblk) + 2 * (bs + u);
-                        dst[0] = dl[r];
-                        dst[1] = dh[r];
-                    }
-                }
-            }
+    };
+    auto b_operand = [&](int u) { return *reinterpret_cast<const long*>(&st.a[u][i16 % BC][2 * g]); };
+    const v4i zero = {0, 0, 0, 0};
+    // The MFMA(s) of block u: its exact int32 sums (q6_K: d[0] for elements 0..15, lanes g < 2, d[1] for 16..31).
+    struct Sums {
+        v4i d[TYPE == Q6_K ? 2 : 1];
+    };
+    auto mfma = [&](long wa, long xa) {
+        Sums r;
+        if constexpr (TYPE == Q6_K) {
+            r.d[0] = __builtin_amdgcn_mfma_i32_16x16x32_i8(g < 2 ? wa : 0L, xa, zero, 0, 0, 0);
+            r.d[1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(g < 2 ? 0L : wa, xa, zero, 0, 0, 0);
         } else {
-            const v4i dd = __builtin_amdgcn_mfma_i32_16x16x32_i8(wa, xa, zero, 0, 0, 0);
-            const float4 dw4 = *reinterpret_cast<const float4*>(&st.dw[u][4 * g]);
-            const float dw[4] = {dw4.x, dw4.y, dw4.z, dw4.w};
-            float dm[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            if constexpr (W::kMins) {
-                const float4 dm4 = *reinterpret_cast<const float4*>(&st.dm[u][4 * g]);
-                dm[0] = dm4.x, dm[1] = dm4.y, dm[2] = dm4.z, dm[3] = dm4.w;
-            }
+            r.d[0] = __builtin_amdgcn_mfma_i32_16x16x32_i8(wa, xa, zero, 0, 0, 0);
+        }
+        return r;
+    };
+    // Each lane's four (row, column) sums of block u scaled into its accumulators. kTail: the last step of a
+    // share shorter than U blocks (the blocks past b1 are skipped).
+    auto epilogue = [&](int bs, int u, const Sums& sm, auto tail_tag) {
+        constexpr bool kTail = decltype(tail_tag)::value;
+        const bool ok = !kTail || bs + u < b1;
+        const float4 xs = st.s[u][i16 % BC];
+        const float4 dw4 = *reinterpret_cast<const float4*>(&st.dw[u][4 * g]);
+        const float dw[4] = {dw4.x, dw4.y, dw4.z, dw4.w};
+        float dm[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (W::kMins) {
+            const float4 dm4 = *reinterpret_cast<const float4*>(&st.dm[u][4 * g]);
+            dm[0] = dm4.x, dm[1] = dm4.y, dm[2] = dm4.z, dm[3] = dm4.w;
+        }
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float v = W::acc(dw[r], dm[r], dd[r], xs, acc[r]);
+        for (int r = 0; r < 4; ++r) {
+            const int m = m0 + 4 * g + r;
+            if constexpr (TYPE == Q6_K) {
+                const float v = W::acc2(dw[r], dm[r], sm.d[0][r], sm.d[1][r], xs, acc[r]);
                 acc[r] = ok ? v : acc[r];
-                if (SUMS) {
-                    const int m = m0 + 4 * g + r;
-                    if (ok && i16 < B && m < M) gs[(size_t(i16) * M + m) * nblk + bs + u] = dd[r];
+                if (SUMS && ok && i16 < B && m < M) {
+                    int32_t* dst = gs + (size_t(i16) * M + m) * (2 * nblk) + 2 * (bs + u);
+                    dst[0] = sm.d[0][r];
+                    dst[1] = sm.d[1][r];
                 }
+            } else {
+                const float v = W::acc(dw[r], dm[r], sm.d[0][r], xs, acc[r]);
+                acc[r] = ok ? v : acc[r];
+                if (SUMS && ok && i16 < B && m < M) gs[(size_t(i16) * M + m) * nblk + bs + u] = sm.d[0][r];
             }
+        }
+    };
+    // The blocks of a step. Phased: every operand of the step read first, then all the MFMAs, then the
+    // epilogues, so the LDS and MFMA latencies of one block overlap the others' (block by block, each block's
+    // reads, MFMA and epilogue form one dependent chain, and 2 waves per SIMD cannot hide it).
+    auto blocks = [&](int bs, int sh, auto tail_tag) {
+        if constexpr (P1X_MMQ_PHASED) {
+            long wa[U], xa[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                wa[u] = a_operand(u, sh);
+                xa[u] = b_operand(u);
+            }
+            Sums sm[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) sm[u] = mfma(wa[u], xa[u]);
+#pragma unroll
+            for (int u = 0; u < U; ++u) epilogue(bs, u, sm[u], tail_tag);
+        } else {
+#pragma unroll P1X_MMQ_UNROLL
+            for (int u = 0; u < U; ++u) epilogue(bs, u, mfma(a_operand(u, sh), b_operand(u)), tail_tag);
         }
     };
     using I0 = std::integral_constant<int, 0>;
@@ -366,13 +391,10 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         load(bs + PF * U, slot_tag);  // in flight while this step and the next compute (past b1: never used)
         const int sh = row_shift(i16, bs);
-        if (bs + U <= b1) {
-#pragma unroll P1X_MMQ_UNROLL
-            for (int u = 0; u < U; ++u) block(bs, u, sh, std::false_type{});
-        } else {
-#pragma unroll P1X_MMQ_UNROLL
-            for (int u = 0; u < U; ++u) block(bs, u, sh, std::true_type{});
-        }
+        if (bs + U <= b1)
+            blocks(bs, sh, std::false_type{});
+        else
+            blocks(bs, sh, std::true_type{});
     };
     if (b0 < b1) {
         load(b0, I0{});
