@@ -130,7 +130,8 @@ KQUANT = [("q4_K", 14336, 4096, (1, 8)), ("q4_K", 4096, 14336, (1,)), ("q6_K", 1
 
 @pytest.mark.parametrize("case", KQUANT, ids=[f"{c[0]}-{c[1]}x{c[2]}" for c in KQUANT])
 def test_config4_kquants(orc, gpu, case):
-    """K-quant matrices at full size: 14336 rows take two rows per wave, 128256 rows four (the output projection)."""
+    """K-quant matrices at full size through the op (Q8_1 pass + kernel): one row per wave at one column (q6_K on
+    rows of 4096-multiples with paired sub-blocks), the int8 matrix cores at 8 columns of q4_K 14336x4096."""
     tname, M, K, cols = case
     t = P.TYPES[tname]
     wd, w = weights(t, M, K, 400 + M)
