@@ -292,7 +292,11 @@ TBO_COLUMNS = ("test_time", "build_commit", "backend_name", "op_name", "op_param
 def tbo_rows(extra):
     """(op_name, op_params, time_us, bytes, flops) for each mat-vec sweep point and FA context in `extra`."""
     rows = []
-    for key, rec in extra.get("matvec_sweep_op_us", {}).items():  # "q4_0 4096x14336 n=1"
+    ops = dict(extra.get("matvec_sweep_op_us", {}))  # "q4_0 4096x14336 n=1": {"us", ...}
+    # The K-quant legs' whole op (Q8_1 pass + kernel), the quantity test-backend-ops times; kernel-only entries
+    # (prepared activation) are not test-backend-ops rows.
+    ops.update({k: v["op"] for k, v in extra.get("kquant", {}).items() if "op" in v})
+    for key, rec in ops.items():
         tname, shape, ncols = key.split()
         m, k = (int(v) for v in shape.split("x"))
         n = int(ncols.split("=")[1])

@@ -16,6 +16,8 @@ EXTRA = {
                            "q8_0 1024x4096 n=8": {"us": 6.5, "gbs": 700.0}},
     "fa_decode": {"by_ctx": {"8192": {"us": 12.47, "bytes": 33587200}}},
     "fa_decode_q4_0_kv": {"by_ctx": {"2048": {"us": 8.04, "bytes": 2392064}}},
+    "kquant": {"q6_K 128256x4096 n=1": {"kernel": {"us": 95.2}, "op": {"us": 97.3, "gbs": 4434.3}},
+               "q6_K 128256x4096 n=8": {"kernel": {"us": 134.8}}},
 }
 
 
@@ -24,12 +26,12 @@ def test_tbo_sql_reads_like_test_backend_ops(tmp_path):
     bench.write_tbo_sql(str(path), EXTRA, "AMD Instinct MI355X")
     text = path.read_text()
     stmts = re.findall(r"(CREATE TABLE.*?\);|INSERT INTO.*?\);)\s*$", text, re.S | re.M)
-    assert len(stmts) == 1 + 4
+    assert len(stmts) == 1 + 5  # the kernel-only K-quant entry is not a test-backend-ops row
     db = sqlite3.connect(":memory:")
     db.executescript("\n".join(stmts))
     rows = db.execute("SELECT op_name, op_params, supported, time_us, bandwidth_gb_s FROM test_backend_ops "
                       "WHERE test_mode='perf'").fetchall()
-    assert len(rows) == 4
+    assert len(rows) == 5
     mm = {}
     for op, params, supported, us, gbs in rows:
         kv = dict(re.findall(r"(\w+)=(\[[^\]]*\]|[^,]+)", params))
@@ -45,3 +47,5 @@ def test_tbo_sql_reads_like_test_backend_ops(tmp_path):
     nbytes = 4096 * 14336 // 32 * 18 + 14336 * 4 + 4096 * 4
     assert abs(gbs - nbytes / (us * 1e-6) / 1e9) < 1e-3
     assert ("q8_0", 1024, 4096, 8) in mm
+    us, gbs = mm[("q6_K", 128256, 4096, 1)]
+    assert us == 97.3 and abs(gbs - (128256 * 4096 // 256 * 210 + 4096 * 4 + 128256 * 4) / 97.3e-6 / 1e9) < 1e-3
