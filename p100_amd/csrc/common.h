@@ -115,6 +115,12 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
 }
 __device__ __forceinline__ float round_fp16(float x) { return __half2float(__float2half(x)); }
 
+// q6_K codes: bits 2j, 2j + 1 of every byte of a qh dword moved to bits 4, 5 (rotated right by 2j - 4 mod 32,
+// one v_alignbit_b32; the mask keeps only bits that came from the same byte), others zero. j = 0..3.
+__device__ __forceinline__ uint32_t q6k_hi2(uint32_t qh, int j) {
+    return __builtin_amdgcn_alignbit(qh, qh, uint32_t(2 * j + 28) & 31u) & 0x30303030u;
+}
+
 // q4_K six-bit scale / min codes of sub-block j (0..7) from the super-block's three scale dwords (bytes 4..15),
 // as get_scale_min_k4 (src/reference/qmv_model.cpp:72-77).
 __device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j, int& sc, int& mn) {

@@ -274,7 +274,7 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_mfma(const uint8_t* __restrict_
             uint32_t v[2];
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
-                const uint32_t c = ((ql[k] >> (4 * (m >> 1))) & 0x0F0F0F0Fu) | (((qh[k] >> (2 * m)) & 0x03030303u) << 4);
+                const uint32_t c = ((ql[k] >> (4 * (m >> 1))) & 0x0F0F0F0Fu) | q6k_hi2(qh[k], m);
                 const uint32_t z = ~c & 0x20202020u;
                 v[k] = (c ^ 0x20202020u) | (z << 2) | (z << 1);
             }

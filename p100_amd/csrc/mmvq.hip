@@ -259,7 +259,7 @@ struct UnitQ6_K32 {
         // from the block's exact isum. The int32 sums are the same integers as those of (v - 32) . x.
         uint32_t v6[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v6[j] = ((ql[j] >> nsh) & kLo) | (((qh[j] >> hsh) & 0x03030303u) << 4);
+        for (int j = 0; j < 8; ++j) v6[j] = ((ql[j] >> nsh) & kLo) | q6k_hi2(qh[j], hsh >> 1);
         constexpr int kOnes = 0x01010101;
         int slo = dot4(kOnes, x[0].lo.x, 0);
         slo = dot4(kOnes, x[0].lo.y, slo);
@@ -331,8 +331,8 @@ struct UnitQ6_K {
         uint32_t va[8], vb[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            va[j] = (ql[j] & kLo) | (((qh[j] >> hsh) & 0x03030303u) << 4);
-            vb[j] = ((ql[j] >> 4) & kLo) | (((qh[j] >> (hsh + 4)) & 0x03030303u) << 4);
+            va[j] = (ql[j] & kLo) | q6k_hi2(qh[j], hsh >> 1);
+            vb[j] = ((ql[j] >> 4) & kLo) | q6k_hi2(qh[j], (hsh >> 1) + 2);
         }
         const float d = half_bits_to_float(dw);
         a = sub(va, x[0], sc[0], d, a, g);
