@@ -34,6 +34,9 @@
 // memory): fa_scratch() looks up each device's address once and the kernels take that pointer.
 static __device__ __align__(256) unsigned char scratch[p1x::kFaScratchBytes];
 
+#ifndef P1X_FA_Q4_HALF
+#define P1X_FA_Q4_HALF 1  // q4_0 cache codes converted two per instruction through fp16
+#endif
 #ifndef P1X_FA_PF
 #define P1X_FA_PF 2  // K/V batches in flight per wave
 #endif
@@ -180,11 +183,27 @@ struct KvQuant {
         } else {
             lo = (lo >> nib_shift) & 0x0F0F0F0Fu;
             hi = (hi >> nib_shift) & 0x0F0F0F0Fu;
+#if P1X_FA_Q4_HALF
+            // Two codes per instruction as fp16: byte b under exponent byte 0x64 is 1024 + b, minus 1024 exact
+            // (the FMAs then read fp16 operands, as for an fp16 cache).
+            const __half2 k1024 = __float2half2_rn(1024.0f);
+            auto two = [&](uint32_t src, uint32_t sel) {
+                return __hsub2(__builtin_bit_cast(__half2, __builtin_amdgcn_perm(0x64646464u, src, sel)), k1024);
+            };
+            const __half2 h[4] = {two(lo, 0x04010400u), two(lo, 0x04030402u), two(hi, 0x04010400u),
+                                  two(hi, 0x04030402u)};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                out[2 * k] = __low2float(h[k]);
+                out[2 * k + 1] = __high2float(h[k]);
+            }
+#else
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 out[k] = float((lo >> (8 * k)) & 0xffu);
                 out[4 + k] = float((hi >> (8 * k)) & 0xffu);
             }
+#endif
         }
         const int d16 = int((w.x >> (8 * doff)) & 0xffffu);  // meaningful in the block's first lane
         const int db = __builtin_amdgcn_update_dpp(0, d16, 0x00, 0xf, 0xf, true);  // quad_perm(0,0,0,0)
