@@ -179,7 +179,7 @@ def test_many_columns_parity(orc, gpu, tname):
 
 
 def _kquant_case(orc, t, w, x, rows, k, nb01=None, offset=0):
-    """q4_K through the fp32 op (with and without group sums) and a prepared activation, the weights at nb01 bytes
+    """A quantized matrix through the fp32 op (with and without group sums) and a prepared activation, the weights at nb01 bytes
     per row from byte `offset` of a device buffer: sums bit-exact, FP32 within the bars, the fp32 op's two calls alike
     bit for bit, and the prepared activation's too on the matrix cores (9..16 columns; at 1..8 the fp32 op may take
     the single-launch dot4 kernel, whose FP32 sums are grouped differently)."""
@@ -272,6 +272,30 @@ def test_q4_K_one_column_register_kernel(orc, gpu):
         check_matvec(orc, t, w, x, y.cpu().numpy(), sums.cpu().numpy(), "q81")
         y2 = P.mul_mat_vec(t, to_dev(w), rows, k, q).cpu().numpy()
         assert (y2.view(np.uint32) == y.cpu().numpy().view(np.uint32)).all()
+
+
+def test_random_shapes_every_form(orc, gpu):
+    """A fixed-seed sweep of 48 shapes over the four types and 1..16 columns (rows 1..300, rows of 1..8 blocks or
+    super-blocks, padded row strides, weights at byte 0 or 4 of their buffer), so the dispatch boundaries between
+    the dot4, register-resident and matrix-core forms meet arbitrary tails: sums bit-exact, FP32 within the bars,
+    the op with and without sums alike bit for bit (the prepared activation too on the matrix cores)."""
+    g = np.random.default_rng(4242)
+    names = ["q4_0", "q8_0", "q4_K", "q6_K"]
+    for case in range(48):
+        tname = names[case % 4]
+        t = orc.TYPES[tname]
+        blk = orc.BLOCK[t][0]
+        k = blk * int(g.integers(1, 9))
+        rows = int(g.integers(1, 301))
+        ncols = int(g.integers(1, 17))
+        w, x = make_case(orc, t, k, rows, ncols, seed=50000 + case)
+        rb = w.shape[1]
+        # Stride padding keeps each type's row alignment (q4_K: 4 bytes, 16 at 9+ columns; others 2 bytes).
+        step = 16 if (tname == "q4_K" and ncols > 8) else (4 if tname == "q4_K" else 2)
+        nb01 = rb + step * int(g.integers(0, 3))
+        offset = 4 * int(g.integers(0, 2))
+        print(f"case {case}: {tname} rows {rows} k {k} ncols {ncols} nb01 {nb01} offset {offset}", flush=True)
+        _kquant_case(orc, t, w, x, rows, k, nb01=nb01, offset=offset)
 
 
 def test_q4_K_many_columns_unaligned_stride(orc, gpu):
