@@ -5,7 +5,8 @@ and the path's stated "max relative error <= 2e-3" read as max|o-ref| / max|ref|
 Inputs are rounded to fp16 (the kernel's K/V type) on the host; Q stays fp32. Shapes: the decode config
 (32 query heads / 8 KV heads, d 128, 1 query row, KV 512..32768, causal), plus GQA ratios 1..8, d 64 / 256,
 batch 2, several query rows with bottom-right causal alignment, masks with fully masked rows, softcap,
-large logits, the error-budget distributions (outlier channels, peaked, biased V) and strided K/V views.
+large logits, the error-budget distributions (outlier channels, peaked, biased V), strided K/V views and a
+fixed-seed sweep of random shapes.
 The reference's analytic cases (tests/test_reference.cpp) run on the GPU with q/k/v zero-padded to d = 64,
 which leaves every dot product and the first d_v output columns unchanged.
 """
@@ -118,6 +119,29 @@ def test_multi_row_causal_and_mask(orc, gpu):
     mask[0, :] = -INF               # a fully masked row
     mask[1, rng.random(200) < 0.7] = -INF
     check(orc, p, q, k, v, mask.ravel())
+
+
+def test_random_shapes(orc, gpu):
+    """A fixed-seed sweep of 32 cases: batch 1..2, KV heads 1..8 with GQA ratios 1..8, d 64 / 128 / 256, 1..4 query
+    rows, 1..3000 keys (split plans from one split to many, partial last batches), causal or not, an additive mask
+    with masked-out keys or none, softcap or none, the default or an explicit scale."""
+    g = np.random.default_rng(777)
+    for case in range(32):
+        hkv = int(g.integers(1, 9))
+        p = orc.AttnParams(batch=int(g.integers(1, 3)), n_head_q=hkv * int(g.integers(1, 9)), n_head_kv=hkv,
+                           seq_q=int(g.integers(1, 5)), seq_kv=int(g.integers(1, 3001)),
+                           d_qk=int(g.choice([64, 128, 256])), causal=bool(g.integers(0, 2)),
+                           softcap=float(g.choice([0.0, 0.0, 4.0])), scale=float(g.choice([0.0, 0.0, 0.3])))
+        p.d_v = p.d_qk
+        mask = None
+        if g.integers(0, 2):
+            mask = (0.5 * g.standard_normal((p.seq_q, p.seq_kv))).astype(np.float32)
+            mask[g.random(mask.shape) < 0.2] = -INF
+            mask = mask.ravel()
+        print(f"case {case}: b {p.batch} hq {p.n_head_q} hkv {hkv} sq {p.seq_q} skv {p.seq_kv} d {p.d_qk} "
+              f"causal {p.causal} mask {mask is not None} softcap {p.softcap} scale {p.scale}", flush=True)
+        q, k, v = gen(orc, p, 9000 + case)
+        check(orc, p, q, k, v, mask)
 
 
 def test_softcap_and_large_logits(orc, gpu):
