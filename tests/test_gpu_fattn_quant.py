@@ -131,6 +131,33 @@ def test_rows_past_device_length_may_hold_nan(orc, gpu, kv_type, n):
         check_len=n, poison=True)
 
 
+def test_random_shapes(orc, gpu):
+    """A fixed-seed sweep of 24 cases: q8_0 or q4_0, batch 1..2, KV heads 1..8 with GQA ratios 1..8, d 64 / 128 /
+    256, 1..4 query rows, 1..3000 keys, causal or not, a mask or none, softcap or none, the dense layout or the
+    interleaved cache view, and (unmasked, non-causal) a device-side length with poisoned rows past it."""
+    g = np.random.default_rng(4343)
+    for case in range(24):
+        kv_type = str(g.choice(KV_TYPES))
+        hkv = int(g.integers(1, 9))
+        seq_q, seq_kv = int(g.integers(1, 5)), int(g.integers(1, 3001))
+        d = int(g.choice([64, 128, 256]))
+        causal = bool(g.integers(0, 2))
+        softcap = float(g.choice([0.0, 0.0, 4.0]))
+        p = orc.AttnParams(int(g.integers(1, 3)), hkv * int(g.integers(1, 9)), hkv, seq_q, seq_kv, d, d,
+                           float(g.choice([0.0, 0.0, 0.3])), softcap, causal)
+        mask, strided, kv_len = None, bool(g.integers(0, 2)), None
+        if g.integers(0, 2):
+            mask = (0.5 * g.standard_normal((seq_q, seq_kv))).astype(np.float32)
+            mask[g.random(mask.shape) < 0.2] = -np.inf
+        elif not causal and not strided and g.integers(0, 2):
+            kv_len = int(g.integers(1, seq_kv + 1))
+        print(f"case {case}: {kv_type} b {p.batch} hq {p.n_head_q} hkv {hkv} sq {seq_q} skv {seq_kv} d {d} "
+              f"causal {causal} mask {mask is not None} softcap {softcap} scale {p.scale} strided {strided} "
+              f"kv_len {kv_len}", flush=True)
+        run(orc, kv_type, p, seed=6000 + case, mask=mask, strided=strided, kv_len=kv_len, check_len=kv_len,
+            poison=kv_len is not None)
+
+
 def test_rejects_bad_arguments(gpu):
     import torch
 
