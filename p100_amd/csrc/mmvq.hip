@@ -60,6 +60,12 @@
 #ifndef P1X_MMVR_Q4_K
 #define P1X_MMVR_Q4_K 1  // one prepared q4_K column on k_mmvr too, on at most 4096 x 4096
 #endif
+#ifndef P1X_MMVR_Q6_K
+#define P1X_MMVR_Q6_K 1  // one prepared q6_K column of 4096..8191 rows of at most 4096: k_mmvr, 2 rows per wave
+#endif
+#ifndef P1X_MMVR_WALK
+#define P1X_MMVR_WALK 768  // and of 8192+ rows: k_mmvr_walk on this many work-groups (0: off)
+#endif
 #ifndef P1X_MMVR_FUSED
 #define P1X_MMVR_FUSED 1  // one f32 q4_0 / q8_0 column in one launch: k_mmvr quantizing x per work-group
 #endif
@@ -850,7 +856,7 @@ struct MmvrPlan {
     int nwk, upt, r;
 };
 bool mmvr_plan(int type, int M, int K, MmvrPlan& p) {
-    const int units = K / (type == Q4_K ? 64 : 32);  // q4_K: sub-block pairs
+    const int units = K / (type == Q4_K || type == kQ6_KPair ? 64 : 32);  // q4_K, q6_K: sub-block pairs
     if (units <= 64) {
         p = {1, 1, 2};
     } else if (units <= 128) {
@@ -906,6 +912,74 @@ hipError_t launch_mmvr(const MmvrPlan& p, const uint8_t* w, int64_t nb01, int M,
     }
 #undef P1X_MMVR
     return hipErrorInvalidValue;
+}
+
+// One prepared column over rows of at most 64 units (one unit per lane): each wave loads its activation blocks
+// once and walks row-groups of R rows (wave w takes groups w, w + waves, ...), with the next group's weights in a
+// second register set while the current one is summed (the loop is unrolled by two so the sets alternate without
+// register copies, which would wait for the loads). Loads past the last group are clamped to row M - 1.
+template <int TYPE, int R, bool SUMS>
+__global__ __launch_bounds__(256) void k_mmvr_walk(const uint8_t* __restrict__ w, int64_t nb01, int M, int K,
+                                                   const int8_t* __restrict__ xq, const float4* __restrict__ xds,
+                                                   float* __restrict__ y, int32_t* __restrict__ gs) {
+    using U = typename UnitOf<TYPE>::T;
+    constexpr int NA = U::kActBlocks;
+    const int lane = threadIdx.x & 63;
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6), nwaves = gridDim.x * 4;
+    const int units = K / U::kElems, ngroups = (M + R - 1) / R;
+    const bool uok = lane < units;
+    const int u = uok ? lane : 0;
+    ActBlock x[NA];
+#pragma unroll
+    for (int ab = 0; ab < NA; ++ab) x[ab] = ActGlobal{xq, xds, K}.get(0, U::act_index(u, ab));
+    auto load = [&](U (&wv)[R], int grp) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) wv[r].load(w + size_t(min(grp * R + r, M - 1)) * nb01, u);
+    };
+    auto sum = [&](const U (&wv)[R], int grp) {
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            int32_t gg[U::kGroups];
+            const float v = wv[r].acc(x, 0.0f, gg);
+            const int row = grp * R + r;
+            if (SUMS && uok && row < M)
+#pragma unroll
+                for (int k = 0; k < U::kGroups; ++k)
+                    gs[size_t(row) * units * U::kGroups + U::group_index(u, k)] = gg[k];
+            acc[r] = wave_total(uok ? v : 0.0f);
+        }
+        if (lane == 0)
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (grp * R + r < M) y[grp * R + r] = acc[r];
+    };
+    U a[R], b[R];
+    int g = wave;
+    if (g >= ngroups) return;
+    load(a, g);
+    for (;;) {
+        load(b, g + nwaves);
+        sum(a, g);
+        g += nwaves;
+        if (g >= ngroups) break;
+        load(a, g + nwaves);
+        sum(b, g);
+        g += nwaves;
+        if (g >= ngroups) break;
+    }
+}
+
+template <int TYPE, int R>
+hipError_t launch_mmvr_walk(int wgs, const uint8_t* w, int64_t nb01, int M, int K, const int8_t* xq,
+                            const float4* xds, float* y, int32_t* gs, hipStream_t stream) {
+    const int groups = (M + R - 1) / R, need = (groups + 3) / 4;
+    const dim3 grid(wgs < need ? wgs : need);
+    if (gs)
+        hipLaunchKernelGGL((k_mmvr_walk<TYPE, R, true>), grid, dim3(256), 0, stream, w, nb01, M, K, xq, xds, y, gs);
+    else
+        hipLaunchKernelGGL((k_mmvr_walk<TYPE, R, false>), grid, dim3(256), 0, stream, w, nb01, M, K, xq, xds, y, gs);
+    return hipGetLastError();
 }
 
 // 2..8 activation columns (q4_0 / q8_0, prepared Q8_1): k_mmvr with B columns. Each thread holds its units' Q8_1
@@ -1165,6 +1239,14 @@ hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int 
         case Q8_0: return launch_type<Q8_0>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
         case Q4_K: return launch_type<Q4_K>(B, wb, nb01, M, K, rw, xq, d4, x, y, gs, stream);
         case Q6_K:
+            // One prepared column on rows of at most 4096 (one paired unit per lane), activation in registers:
+            // 8192+ rows walk row by row on 768 work-groups (128256x4096 95-96 -> 82 us, 14336x4096 13.6 -> 12.9),
+            // 4096..8191 rows take k_mmvr at 2 rows per wave (4096x4096 6.1 -> 5.5-5.95 us). On 1024 rows both
+            // are slower than the LDS-staged kernel (3.5 against 3.7 us).
+            if (P1X_MMVR_WALK && B == 1 && !x && K <= 4096 && M >= 8192)
+                return launch_mmvr_walk<kQ6_KPair, 1>(P1X_MMVR_WALK, wb, nb01, M, K, xq, d4, y, gs, stream);
+            if (P1X_MMVR_Q6_K && B == 1 && !x && K <= 4096 && M >= 4096 && mmvr_plan(kQ6_KPair, M, K, plan))
+                return launch_mmvr<kQ6_KPair>(plan, wb, nb01, M, K, SrcQ81{xq, d4}, EpiRows{y, nullptr}, gs, stream);
             // One column on rows of whole 64-unit passes: the paired unit (128256x4096 105.5 -> 95.1 us, 14336x4096
             // 14.2 -> 13.6); on 14336-long rows (3.5 passes) and at 2+ columns (twice the activation registers) the
             // one-sub-block unit is faster (4096x14336 15.8 against 18.9 us).

@@ -274,6 +274,31 @@ def test_q4_K_one_column_register_kernel(orc, gpu):
         assert (y2.view(np.uint32) == y.cpu().numpy().view(np.uint32)).all()
 
 
+def test_q6_K_one_column_register_kernels(orc, gpu):
+    """One q6_K column on a prepared activation with rows of at most 4096 keeps the activation in registers (one
+    unit of two sub-blocks per lane): 8192+ rows walk row by row (k_mmvr_walk: each wave takes rows w, w + waves,
+    ...; the last wave's surplus loads clamped to the last row), 4096..8191 rows take k_mmvr at two rows per wave.
+    Row counts that leave partial last rounds, rows of 1..16 super-blocks (idle lanes), a padded row stride and a
+    base at byte 4 of the buffer; group sums bit-exact, FP32 within the bars, with and without the sum export bit for bit."""
+    import p100_amd as P
+
+    t = orc.TYPES["q6_K"]
+    for k, rows, pad, offset in ((4096, 8197, 0, 0), (256, 9001, 0, 0), (1280, 8200, 6, 4), (4096, 4099, 0, 0),
+                                 (512, 5000, 6, 4), (3840, 12289, 0, 0)):
+        w, x = make_case(orc, t, k, rows, 1, seed=3900 + k + rows)
+        rb = w.shape[1]
+        nb01 = rb + pad
+        buf = np.zeros(offset + rows * nb01, np.uint8)
+        buf[offset:].reshape(rows, nb01)[:, :rb] = w
+        wd = to_dev(buf)[offset:]
+        print(f"q6_K rows {rows} k {k} nb01 {nb01} offset {offset}", flush=True)
+        q = P.quantize_q8_1(to_dev(x))
+        y, sums = P.mul_mat_vec(t, wd, rows, k, q, nb01=nb01, group_sums=True)
+        check_matvec(orc, t, w, x, y.cpu().numpy(), sums.cpu().numpy(), "q81")
+        y2 = P.mul_mat_vec(t, wd, rows, k, q, nb01=nb01).cpu().numpy()
+        assert (y2.view(np.uint32) == y.cpu().numpy().view(np.uint32)).all()
+
+
 def test_random_shapes_every_form(orc, gpu):
     """A fixed-seed sweep of 48 shapes over the four types and 1..16 columns (rows 1..300, rows of 1..8 blocks or
     super-blocks, padded row strides, weights at byte 0 or 4 of their buffer), so the dispatch boundaries between
