@@ -66,6 +66,9 @@
 #ifndef P1X_MMVR_WALK
 #define P1X_MMVR_WALK 768  // and of 8192+ rows: k_mmvr_walk on this many work-groups (0: off)
 #endif
+#ifndef P1X_MMVR_WALK_Q4_K
+#define P1X_MMVR_WALK_Q4_K 65536  // one prepared q4_K column of this many rows (or more) of at most 4096 too
+#endif
 #ifndef P1X_MMVR_FUSED
 #define P1X_MMVR_FUSED 1  // one f32 q4_0 / q8_0 column in one launch: k_mmvr quantizing x per work-group
 #endif
@@ -1228,6 +1231,11 @@ hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int 
     // q4_K units are sub-block pairs with two Q8_1 blocks each, so every wave of k_mmvr reads 96 activation bytes
     // per unit from L2: faster than the LDS-staged kernel on 4096x4096 (4.37 against 4.62 us) and 1024x4096
     // (2.97 / 3.06), slower on 14336x4096 (9.73 / 8.99) and 4096x14336 (11.13 / 9.85).
+    // A tall q4_K matrix walks too (128256x4096 59.5-61.7 -> 57.2-57.8 us); on 14336 rows it was slower than the
+    // LDS-staged kernel (9.1 against 8.95 us).
+    if (P1X_MMVR_WALK > 0 && P1X_MMVR_WALK_Q4_K > 0 && B == 1 && !x && type == Q4_K && K <= 4096 &&
+        M >= P1X_MMVR_WALK_Q4_K)
+        return launch_mmvr_walk<Q4_K, 1>(P1X_MMVR_WALK, wb, nb01, M, K, xq, d4, y, gs, stream);
     if (B == 1 && !x && P1X_MMVR_ENABLE && P1X_MMVR_Q4_K && type == Q4_K && M <= 4096 && K <= 4096 &&
         mmvr_plan(type, M, K, plan))
         return launch_mmvr<Q4_K>(plan, wb, nb01, M, K, SrcQ81{xq, d4}, EpiRows{y, nullptr}, gs, stream);
@@ -1243,7 +1251,7 @@ hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int 
             // 8192+ rows walk row by row on 768 work-groups (128256x4096 95-96 -> 82 us, 14336x4096 13.6 -> 12.9),
             // 4096..8191 rows take k_mmvr at 2 rows per wave (4096x4096 6.1 -> 5.5-5.95 us). On 1024 rows both
             // are slower than the LDS-staged kernel (3.5 against 3.7 us).
-            if (P1X_MMVR_WALK && B == 1 && !x && K <= 4096 && M >= 8192)
+            if (P1X_MMVR_WALK > 0 && B == 1 && !x && K <= 4096 && M >= 8192)
                 return launch_mmvr_walk<kQ6_KPair, 1>(P1X_MMVR_WALK, wb, nb01, M, K, xq, d4, y, gs, stream);
             if (P1X_MMVR_Q6_K && B == 1 && !x && K <= 4096 && M >= 4096 && mmvr_plan(kQ6_KPair, M, K, plan))
                 return launch_mmvr<kQ6_KPair>(plan, wb, nb01, M, K, SrcQ81{xq, d4}, EpiRows{y, nullptr}, gs, stream);
