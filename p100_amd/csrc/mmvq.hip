@@ -58,7 +58,7 @@
 #define P1X_MMVR_ENABLE 1  // one prepared q4_0 / q8_0 column: register-resident activation kernel (k_mmvr)
 #endif
 #ifndef P1X_MMVR_Q4_K
-#define P1X_MMVR_Q4_K 1  // one prepared q4_K column on k_mmvr too, on at most 4096 x 4096
+#define P1X_MMVR_Q4_K 1  // one prepared q4_K column of at most 4096 rows on k_mmvr too (rows up to 16384)
 #endif
 #ifndef P1X_MMVR_Q6_K
 #define P1X_MMVR_Q6_K 1  // one prepared q6_K column of 4096..8191 rows of at most 4096: k_mmvr, 2 rows per wave
@@ -902,6 +902,9 @@ hipError_t launch_mmvr(const MmvrPlan& p, const uint8_t* w, int64_t nb01, int M,
         P1X_MMVR(2, 2, 2)
     } else {
         P1X_MMVR(1, 1, 2)
+        if constexpr (TYPE == Q4_K) {
+            P1X_MMVR(4, 1, 4)
+        }
         if constexpr (!EPI::kPairs) {
             P1X_MMVR(1, 2, 1)
         }
@@ -1236,6 +1239,11 @@ hipError_t launch_mmvq(int type, int B, const void* w, int64_t nb01, int M, int 
     if (P1X_MMVR_WALK > 0 && P1X_MMVR_WALK_Q4_K > 0 && B == 1 && !x && type == Q4_K && K <= 4096 &&
         M >= P1X_MMVR_WALK_Q4_K)
         return launch_mmvr_walk<Q4_K, 1>(P1X_MMVR_WALK, wb, nb01, M, K, xq, d4, y, gs, stream);
+    // Rows of 4097..16384 q4_K elements: four waves per row at one unit per thread and four rows per work-group,
+    // so each wave reads its activation blocks for four rows (4096x14336 9.79-9.89 -> 9.52-9.58 us; two units per
+    // thread and two or four rows, or four waves and two rows: 10.3 / 11.2 us).
+    if (B == 1 && !x && P1X_MMVR_ENABLE && P1X_MMVR_Q4_K && type == Q4_K && M <= 4096 && K > 4096 && K <= 16384)
+        return launch_mmvr<Q4_K>(MmvrPlan{4, 1, 4}, wb, nb01, M, K, SrcQ81{xq, d4}, EpiRows{y, nullptr}, gs, stream);
     if (B == 1 && !x && P1X_MMVR_ENABLE && P1X_MMVR_Q4_K && type == Q4_K && M <= 4096 && K <= 4096 &&
         mmvr_plan(type, M, K, plan))
         return launch_mmvr<Q4_K>(plan, wb, nb01, M, K, SrcQ81{xq, d4}, EpiRows{y, nullptr}, gs, stream);

@@ -260,14 +260,16 @@ def test_q6_K_few_columns_matrix_cores(orc, gpu):
 
 def test_q4_K_one_column_register_kernel(orc, gpu):
     """One q4_K column on a prepared activation up to 4096 x 4096 runs the register-resident kernel (k_mmvr with
-    sub-block-pair units, two Q8_1 blocks each), and from 65536 rows of at most 4096 the walking form
-    (k_mmvr_walk): group sums bit-exact and FP32 within the bars, with and without the sum export bit for bit; a
-    row tail (rows not a multiple of the work-group's 8, a partial last round of the walk) and one super-block
-    rows."""
+    sub-block-pair units, two Q8_1 blocks each), rows of 4097..16384 elements on four waves per row (up to 256
+    units, one per thread), and from 65536 rows of at most 4096 the walking form (k_mmvr_walk): group sums
+    bit-exact and FP32 within the bars, with and without the sum export bit for bit; a row tail (rows not a
+    multiple of the work-group's rows, a partial last round of the walk), one super-block rows and rows that
+    leave 1..188 threads idle."""
     import p100_amd as P
 
     t = orc.TYPES["q4_K"]
-    for k, rows in ((4096, 4096), (4096, 1027), (256, 40), (2048, 17), (256, 65541), (768, 65600)):
+    for k, rows in ((4096, 4096), (4096, 1027), (256, 40), (2048, 17), (256, 65541), (768, 65600), (14336, 1027),
+                    (16384, 40), (4352, 17)):
         w, x = make_case(orc, t, k, rows, 1, seed=3800 + k + rows)
         q = P.quantize_q8_1(to_dev(x))
         y, sums = P.mul_mat_vec(t, to_dev(w), rows, k, q, group_sums=True)
