@@ -303,6 +303,26 @@ def test_q6_K_one_column_register_kernels(orc, gpu):
         assert (y2.view(np.uint32) == y.cpu().numpy().view(np.uint32)).all()
 
 
+@pytest.mark.parametrize("tname,k,rows", [
+    ("q6_K", 256, 4095), ("q6_K", 256, 4096), ("q6_K", 512, 8191), ("q6_K", 512, 8192),
+    ("q4_K", 256, 65535), ("q4_K", 256, 65536), ("q4_K", 4352, 4096), ("q4_K", 4352, 4097),
+    ("q4_K", 4096, 4097)])
+def test_kquant_one_column_dispatch_boundaries(orc, gpu, tname, k, rows):
+    """One prepared K-quant column on each side of the row and row-length thresholds where the kernel changes
+    (q6_K: LDS-staged below 4096 rows, k_mmvr to 8191, the walk from 8192; q4_K: the walk from 65536 rows, the
+    four-wave form for rows of 4097..16384 elements up to 4096 rows): sums bit-exact, FP32 within the bars, the
+    same bits without the sum export."""
+    import p100_amd as P
+
+    t = orc.TYPES[tname]
+    w, x = make_case(orc, t, k, rows, 1, seed=4100 + k + rows)
+    q = P.quantize_q8_1(to_dev(x))
+    y, sums = P.mul_mat_vec(t, to_dev(w), rows, k, q, group_sums=True)
+    check_matvec(orc, t, w, x, y.cpu().numpy(), sums.cpu().numpy(), "q81")
+    y2 = P.mul_mat_vec(t, to_dev(w), rows, k, q).cpu().numpy()
+    assert (y2.view(np.uint32) == y.cpu().numpy().view(np.uint32)).all()
+
+
 def test_random_shapes_every_form(orc, gpu):
     """A fixed-seed sweep of 48 shapes over the four types and 1..16 columns (rows 1..300, rows of 1..8 blocks or
     super-blocks, padded row strides, weights at byte 0 or 4 of their buffer), so the dispatch boundaries between
